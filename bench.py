@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""Benchmark: µs per RMSNorm + W4A16 MoE layer at a 256-token canvas, on one MI355X.
+
+Workload layer_256: x bf16 [256, 2816] -> RMSNorm (w bf16 [2816], eps 1e-6) ->
+W4A16 MoE (128 experts, top-8 from softmax of N(0,1) logits, renormalised;
+gate/up [1408, 2816] group 128, down [2816, 704] group 64, asymmetric uint4,
+fp16 scale/zero; SiLU-gated) -> fixed-order combine -> bf16 [256, 2816].
+Synthetic seeded data. Inputs are resident in HBM before the timed region.
+
+A "step" is one layer. Consecutive steps rotate over independent weight sets
+(3 x 412 MB by default) so the 256 MB MALL cannot serve weights from cache.
+
+Timed passes (all inside this process, same stream):
+  1. value: K steps of the layer (two C calls per step: RMSNorm, fused MoE
+     forward), bracketed by synchronize; µs per layer = elapsed / K.
+  2. per-kernel: K steps issued stage by stage with HIP events between the
+     five launches; the average duration of each kernel, from which the
+     dominant kernel's achieved bandwidth (roofline) is computed.
+  3. cpu_baseline: the reference CPU path (torch eager, oracle/cpu_baseline.py)
+     on the host cores, bounded to ~20 s.
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+PKG = "knivesysl-diffusion-xe_amd"
+
+METRIC = "µs per RMSNorm+W4A16 MoE layer at 256-tok canvas; achieved HBM GB/s (% peak)"
+HBM_PEAK_GBPS = 8000.0
+
+T, TOPK, E, H, I = 256, 8, 128, 2816, 704
+GU_EXPERT_BYTES = 2 * I * (H // 2) + 2 * (2 * I * (H // 128) * 2)  # 1,982,464 + 123,904
+DN_EXPERT_BYTES = H * (I // 2) + 2 * (H * (I // 64) * 2)           # 991,232 + 123,904
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_algorithmic_bytes(n_experts_touched: int) -> int:
+    """Compulsory HBM bytes of one layer: weights of every touched expert, the
+    norm's input/weight/output, the MoE input and output, and the routing
+    (ids int64 + weights fp32)."""
+    w = n_experts_touched * (GU_EXPERT_BYTES + DN_EXPERT_BYTES)
+    norm = T * H * 2 + H * 2 + T * H * 2
+    moe_io = T * H * 2 + T * H * 2 + T * TOPK * (8 + 4)
+    return w + norm + moe_io
+
+
+def gateup_algorithmic_bytes(n_experts_touched: int) -> int:
+    """Compulsory bytes of one gate/up launch: touched experts' gate/up weights,
+    the fp16 activations read once, out2 written, sorted rows and offsets."""
+    return (n_experts_touched * GU_EXPERT_BYTES + T * H * 2 + T * TOPK * I * 2 + T * TOPK * 4 + (E + 1) * 4)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--weight-sets", type=int, default=3)
+    ap.add_argument("--act", choices=["silu", "gelu"], default="silu")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--skip-kernel-pass", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py measures one MI355X: this build runs the layer on a single GPU and has no "
+            "multi-GPU path (see DESIGN.md for how the layer would shard). Run with --gpus 1.")
+        return 2
+
+    import torch
+    pkg = importlib.import_module(PKG)
+    wl = importlib.import_module(f"{PKG}.workloads")
+    layer_mod = importlib.import_module(f"{PKG}.layer")
+    lib = pkg._lib
+    L = lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] device {torch.cuda.get_device_name(0)}; building inputs")
+
+    x, nw, ids, w = wl.layer_inputs(T, 3)
+    xg, nwg, idsg, wg = x.to(dev), nw.to(dev), ids.to(dev), w.to(dev)
+    sets = []
+    for s in range(args.weight_sets):
+        exp = wl.make_experts(E, H, I, 100 + s, act=args.act, device=dev)
+        sets.append(exp)
+    n_touched = int(torch.unique(ids).numel())
+    torch.cuda.synchronize()
+    log(f"[bench] {args.weight_sets} weight sets x {sets[0].nbytes() / 1e6:.1f} MB; experts touched {n_touched}")
+
+    runner = layer_mod.LayerRunner(T, TOPK, E, H, I, dev)
+    ws = torch.empty(int(L.ksl_moe_workspace_bytes(T, TOPK, E, H, I)), dtype=torch.uint8, device=dev)
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    xn = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    p = lib.ptr
+    st = lib.stream_of(xg)
+    v2 = importlib.import_module(f"{PKG}.fused_moe_w4_v2")
+    for exp in sets:
+        v2._check_act(exp)
+        v2._check_weights(exp, E, H, I)
+
+    def step(exp):
+        rc = L.ksl_rmsnorm(p(xg), lib.DTYPE_BF16, p(nwg), lib.DTYPE_BF16, p(xn), lib.DTYPE_BF16, T, H, H, H,
+                           1e-6, st)
+        if rc:
+            lib.check(rc, "ksl_rmsnorm")
+        rc = L.ksl_moe_w4a16_forward(p(xn), lib.DTYPE_BF16, H, p(idsg), p(wg), lib.DTYPE_F32,
+                                     p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z),
+                                     T, TOPK, E, H, I, exp._ksl_act, p(y), lib.DTYPE_BF16, H,
+                                     p(ws), ws.numel(), st)
+        if rc:
+            lib.check(rc, "ksl_moe_w4a16_forward")
+
+    # ---- pass 1: whole-layer time -------------------------------------------
+    for i in range(args.warmup):
+        step(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        step(sets[i % len(sets)])
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev_ms = e0.elapsed_time(e1)
+    ms_per_step = ev_ms / args.steps
+    layer_us = ms_per_step * 1e3
+    layer_bytes = layer_algorithmic_bytes(n_touched)
+    layer_gbps = layer_bytes / (layer_us * 1e-6) / 1e9
+    log(f"[bench] layer: {layer_us:.2f} us/step (events), wall {wall_ms / args.steps * 1e3:.2f} us/step; "
+        f"{layer_gbps:.0f} GB/s = {100 * layer_gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
+
+    # ---- pass 2: per-kernel durations with events between launches ----------
+    kernels = {}
+    if not args.skip_kernel_pass:
+        stages = layer_mod.STAGES
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(args.steps)]
+        for i in range(args.warmup):
+            runner.run(xg, nwg, 1e-6, sets[i % len(sets)], idsg, wg)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            runner.run(xg, nwg, 1e-6, sets[i % len(sets)], idsg, wg, events=evs[i])
+        torch.cuda.synchronize()
+        for k, name in enumerate(stages):
+            d = sorted(evs[i][k].elapsed_time(evs[i][k + 1]) * 1e3 for i in range(args.steps))
+            kernels[name] = {"avg_us": sum(d) / len(d), "median_us": d[len(d) // 2]}
+        tot = sum(v["avg_us"] for v in kernels.values())
+        log("[bench] per-kernel avg us: " + ", ".join(f"{k} {v['avg_us']:.2f}" for k, v in kernels.items())
+            + f" (sum {tot:.2f})")
+        # parity of the staged output with the fused call on the same set
+        step(sets[0])
+        yf = y.clone()
+        ys = runner.run(xg, nwg, 1e-6, sets[0], idsg, wg).clone()
+        torch.cuda.synchronize()
+        if not torch.equal(yf.view(torch.int16), ys.view(torch.int16)):
+            log("[bench] WARNING: staged and fused outputs differ")
+
+    gu_bytes = gateup_algorithmic_bytes(n_touched)
+    roofline = None
+    if kernels:
+        gu_us = kernels["gateup"]["avg_us"]
+        ach = gu_bytes / (gu_us * 1e-6) / 1e9
+        traffic = None
+        tpath = os.path.join(ROOT, "profiles", "traffic_moe_gateup_layer256.json")
+        if os.path.exists(tpath):
+            with open(tpath) as f:
+                traffic = json.load(f).get("hbm_bytes_per_launch")
+        roofline = {"kernel": "gateup_act_kernel", "bound": "hbm", "achieved": round(ach, 1),
+                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                    "traffic": traffic, "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 3)}
+
+    # ---- pass 3: CPU baseline ------------------------------------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline as cb
+        log("[bench] cpu baseline (torch eager on host cores)...")
+        expc = sets[0].to("cpu")
+        act_code = 1 if args.act == "silu" else 0
+        r = cb.time_layer(x, nw, 1e-6, expc, ids, w, act_code, budget_s=args.cpu_budget)
+        cpu = {"value": round(r["dequant_per_call_s"] * 1e6, 1), "unit": "us", "cores": r["threads"],
+               "kind": "port",
+               "sample": (f"full layer_256 (all {E} experts), median of {r['dequant_per_call_runs']} runs "
+                          f"after 1 warm-up, dequant per call; pre-dequantised weights: "
+                          f"{r['predequant_s'] * 1e6:.0f} us (median of {r['predequant_runs']})"),
+               "predequant_us": round(r["predequant_s"] * 1e6, 1)}
+        log(f"[bench] cpu: {cpu['value']:.0f} us/layer dequant-per-call, {cpu['predequant_us']:.0f} us pre-dequantised, "
+            f"{r['threads']} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(layer_us, 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"layer_256: RMSNorm bf16 [{T},{H}] + W4A16 MoE E={E} top-{TOPK} H={H} I={I} "
+                         f"gu gs128 / dn gs64, {args.act}, fixed-order combine -> bf16"),
+            "tokens": T, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I,
+            "act": args.act, "weight_sets": args.weight_sets, "experts_touched": n_touched,
+            "layer_algorithmic_bytes": layer_bytes,
+            "layer_GBps": round(layer_gbps, 1),
+            "layer_frac_of_hbm_peak": round(layer_gbps / HBM_PEAK_GBPS, 4),
+            "compute": "u4 weights, f16 MFMA operands, f32 accumulate, bf16 in/out",
+            "parallelism": "single GPU",
+            "kernels_us": {k: round(v["avg_us"], 3) for k, v in kernels.items()},
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,130 @@
+/* C ABI of the MI355X (gfx950) fused layer-kernel library: RMSNorm and the
+ * W4A16 128-expert fused MoE forward of the DiffusionGemma block-diffusion
+ * model.
+ *
+ * Every entry point takes raw device pointers, element counts and strides and
+ * the HIP stream to launch on (hipStream_t passed as void*). Every entry point
+ * returns 0 on success or a KSL_ERR_* code, never throws, never synchronises
+ * the host and never allocates device memory: buffers come from the caller.
+ * Outputs are written in full by the launched kernels.
+ *
+ * Reference interfaces are cited as path:line in SRSWTI/knivesysl-diffusion-xe.
+ */
+#ifndef KSL_H_
+#define KSL_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define KSL_OK 0
+#define KSL_ERR_ARG 1       /* null pointer or bad enum */
+#define KSL_ERR_SHAPE 2     /* shape / divisibility contract violated */
+#define KSL_ERR_ALIGN 3     /* pointer or stride alignment contract violated */
+#define KSL_ERR_LAUNCH 4    /* kernel launch failed */
+#define KSL_ERR_WORKSPACE 5 /* workspace too small */
+
+/* storage dtype codes */
+#define KSL_DTYPE_F32 0
+#define KSL_DTYPE_F16 1
+#define KSL_DTYPE_BF16 2
+
+/* activation codes for the gate/up epilogue */
+#define KSL_ACT_GELU_TANH 0 /* kernels/fused_moe_w4_v2.py:136-138 */
+#define KSL_ACT_SILU 1      /* SiLU-gated variant (act(g) = g * sigmoid(g)) */
+
+/* Library version (bumped on ABI changes). */
+int ksl_version(void);
+
+/* Human-readable text of a status code. */
+const char* ksl_status_string(int status);
+
+/* RMSNorm over the last dim, one launch.
+ * Replaces fused_rmsnorm / _rmsnorm_kernel (kernels/fused_rmsnorm.py:10-32).
+ * y[r, :] = to(y_dtype)( bf16( x * (1/sqrt(sum(x^2)/cols + eps)) [* w] ) )
+ * x: [rows, cols] with row stride x_stride (elements); w: [cols] or NULL
+ * (a norm without scale, kernels/fused_rmsnorm.py:35-36); y: [rows, cols]
+ * with row stride y_stride. The value is always rounded to bf16 first, as the
+ * reference stores bf16 and then casts to x.dtype (fused_rmsnorm.py:21, :32).
+ * fp32 accumulation. */
+int ksl_rmsnorm(const void* x, int x_dtype, const void* w, int w_dtype, void* y, int y_dtype,
+                int64_t rows, int64_t cols, int64_t x_stride, int64_t y_stride, float eps,
+                void* stream);
+
+/* Routing metadata on the GPU, one launch.
+ * Replaces moe_align (kernels/fused_moe_w4.py:15-51) with identical outputs:
+ *   sorted_rows int64[cap]    expanded row (t*topk + slot) per sorted slot,
+ *                             pad slots = T*topk
+ *   expert_ids  int64[max_blocks]  expert of each block_m block, pad = E
+ *   inv         int64[T*topk] sorted slot of each expanded row (dropped: 0)
+ * with max_blocks = ceil(T*topk/block_m) + E and cap = max_blocks*block_m.
+ * Ids are clamped to <= E (E marks a dropped row); a negative id is treated
+ * as dropped (the reference raises an index error there). E <= 512. */
+int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
+                  int64_t* sorted_rows, int64_t* expert_ids, int64_t* inv, void* stream);
+
+/* Workspace bytes the fused forward needs for these shapes. */
+size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I);
+
+/* The whole W4A16 MoE forward, five launches, no host sync.
+ * Replaces fused_moe_w4_v2 (kernels/fused_moe_w4_v2.py:319-371):
+ *   align -> gate/up + activation -> down -> fixed-order top-k combine.
+ * hidden: [T, H] (bf16/fp16/fp32) with row stride hidden_stride;
+ * topk_ids int64 [T, topk]; topk_w [T, topk] (fp32/fp16/bf16);
+ * gu_q uint8 [E, 2I, H/2], gu_s/gu_z fp16 [E, 2I, H/128];
+ * dn_q uint8 [E, H, I/2],  dn_s/dn_z fp16 [E, H, I/64]  (all contiguous;
+ * zero-points are integers in [0, 15] as quantize_w4 writes them,
+ * kernels/w4a16.py:28);
+ * y: [T, H] of y_dtype with row stride y_stride. H % 128 == 0, I % 64 == 0
+ * (fused_moe_w4_v2.py:327-328). */
+int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_stride,
+                          const int64_t* topk_ids, const void* topk_w, int w_dtype,
+                          const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z,
+                          int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
+                          void* y, int y_dtype, int64_t y_stride,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- the forward's stages, exposed for tests and for callers that fuse
+ *      their own pipeline (same kernels as ksl_moe_w4a16_forward) ---------- */
+
+/* Compact routing (moe_align with block_m = 1, int32): rows of expert e occupy
+ * sorted slots [offsets[e], offsets[e+1]); sorted_rows int32[T*topk] (tail
+ * past offsets[E] = T*topk); inv int32[T*topk]. Plus, in the same launch, the
+ * fp16 activation copy a16[T, H] (hidden.to(fp16), fused_moe_w4_v2.py:347)
+ * stored with each 8-element block in MFMA K-slot order {0,4,1,5,2,6,3,7}.
+ * a16 may be NULL (routing only). */
+int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                  int32_t* sorted_rows, int32_t* offsets, int32_t* inv,
+                  const void* hidden, int hidden_dtype, int64_t hidden_stride, int64_t H,
+                  void* a16, void* stream);
+
+/* Grouped W4 gate/up GEMM with the activation fused in the epilogue.
+ * Replaces _gateup_act_kernel (kernels/fused_moe_w4_v2.py:96-139).
+ * out2 fp16 [T*topk, I] row per sorted slot, 8-blocks in K-slot order. */
+int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
+                       int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                       int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
+
+/* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
+ * out3 fp16 [T*topk, H] row per sorted slot, natural column order. */
+int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
+                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, void* stream);
+
+/* Fixed-order top-k combine, no atomics: y[t,:] = fma-chain over k=0..topk-1
+ * of fp32(w[t,k]) * fp32(out3[inv[t*topk+k], :]), rounded once to y_dtype.
+ * Replaces _combine_kernel / _combine (kernels/fused_moe_w4_v2.py:248-288).
+ * H % 8 == 0. */
+int ksl_moe_combine(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                    int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KSL_H_ */

@@ -1,0 +1,17 @@
+"""MI355X (gfx950) fused layer kernels for the DiffusionGemma W4A16 MoE.
+
+Drop-in modules, named after the reference's kernel modules:
+  fused_rmsnorm    fused_rmsnorm, _fused_forward, patch_rmsnorms
+  fused_moe_w4     moe_align (GPU routing metadata)
+  fused_moe_w4_v2  fused_moe_w4_v2 (W4A16 128-expert fused MoE forward)
+  pack_experts     fused_experts_forward, GU_GS, DN_GS
+  layer            moe_layer: RMSNorm followed by the MoE forward
+All compute runs in libksl.so (hand-written HIP, C ABI in include/ksl.h).
+"""
+from . import _lib
+from .fused_moe_w4 import moe_align
+from .fused_moe_w4_v2 import fused_moe_w4_v2
+from .fused_rmsnorm import fused_rmsnorm, patch_rmsnorms
+from .pack_experts import fused_experts_forward
+
+__all__ = ["fused_rmsnorm", "patch_rmsnorms", "moe_align", "fused_moe_w4_v2", "fused_experts_forward"]

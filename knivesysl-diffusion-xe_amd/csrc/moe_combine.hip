@@ -1,0 +1,178 @@
+// Fixed-order top-k combine and the fused forward's orchestration.
+//
+// Combine (kernels/fused_moe_w4_v2.py:248-263): for each token t and column,
+// acc = 0; for k = 0..topk-1: acc = fma(fp32(w[t,k]), fp32(out3[inv[t*topk+k]]), acc);
+// y = round(acc). No atomics; the order is the top-k slot order, so the output
+// is bit-identical run to run. Each thread owns 8 consecutive columns of one
+// token (128-bit loads of out3, 128-bit stores of y).
+#include "ksl_common.h"
+
+namespace ksl {
+
+int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
+                  int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
+                  int64_t H, void* a16, hipStream_t st);
+int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
+                  const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
+                  int64_t I, int act, void* out2, hipStream_t st);
+int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
+                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st);
+
+namespace {
+
+constexpr int kCombThreads = 256;
+
+template <int WD, int YD>
+__global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __restrict__ out3,
+                                                              const int32_t* __restrict__ inv,
+                                                              const void* __restrict__ wv, int64_t T,
+                                                              int topk, int64_t H, void* __restrict__ yv,
+                                                              int64_t ys) {
+    typedef typename Elem<WD>::T WT;
+    typedef typename Elem<YD>::T YT;
+    const WT* w = static_cast<const WT*>(wv);
+    YT* y = static_cast<YT*>(yv);
+    const int64_t hv = H / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kCombThreads + threadIdx.x;
+    const int64_t t = idx / hv;
+    if (t >= T) return;
+    const int64_t c0 = (idx - t * hv) * 8;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+        const int64_t r = inv[t * topk + k];
+        const float wk = Elem<WD>::load(w + t * topk + k);
+        const f16x8 x = *reinterpret_cast<const f16x8*>(out3 + r * H + c0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wk, static_cast<float>(x[j]), acc[j]);
+    }
+    store8<YD>(y + t * ys + c0, acc);
+}
+
+template <int WD>
+int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w, int64_t T,
+                     int64_t topk, int64_t H, void* y, int64_t ys, hipStream_t st) {
+    const int64_t n = T * (H / 8);
+    const unsigned grid = static_cast<unsigned>((n + kCombThreads - 1) / kCombThreads);
+    const f16* o3 = static_cast<const f16*>(out3);
+    switch (yd) {
+        case KSL_DTYPE_BF16:
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_BF16>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+                               inv, w, T, static_cast<int>(topk), H, y, ys);
+            break;
+        case KSL_DTYPE_F16:
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F16>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+                               inv, w, T, static_cast<int>(topk), H, y, ys);
+            break;
+        case KSL_DTYPE_F32:
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F32>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+                               inv, w, T, static_cast<int>(topk), H, y, ys);
+            break;
+        default:
+            return KSL_ERR_ARG;
+    }
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+
+}  // namespace
+
+int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
+                   int64_t topk, int64_t H, void* y, int yd, int64_t ys, hipStream_t st) {
+    if (!out3 || !inv || !w || !y) return T == 0 ? KSL_OK : KSL_ERR_ARG;
+    if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0 || ys < H) return KSL_ERR_SHAPE;
+    if (ys % 8 != 0 || reinterpret_cast<uintptr_t>(out3) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
+        return KSL_ERR_ALIGN;
+    if (T == 0) return KSL_OK;
+    switch (wd) {
+        case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16>(yd, out3, inv, w, T, topk, H, y, ys, st);
+    }
+    return KSL_ERR_ARG;
+}
+
+// Workspace layout of the fused forward (each region 256-byte aligned):
+//   sorted_rows i32[Nexp] | offsets i32[E+1] | inv i32[Nexp] |
+//   a16 f16[T*H] | out2 f16[Nexp*I] | out3 f16[Nexp*H]
+struct MoeWorkspace {
+    size_t sorted_rows, offsets, inv, a16, out2, out3, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+static MoeWorkspace moe_workspace_layout(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
+    MoeWorkspace w;
+    const size_t nexp = static_cast<size_t>(T * topk);
+    size_t off = 0;
+    w.sorted_rows = off; off += align256(nexp * 4);
+    w.offsets = off;     off += align256(static_cast<size_t>(E + 1) * 4);
+    w.inv = off;         off += align256(nexp * 4);
+    w.a16 = off;         off += align256(static_cast<size_t>(T * H) * 2);
+    w.out2 = off;        off += align256(nexp * static_cast<size_t>(I) * 2);
+    w.out3 = off;        off += align256(nexp * static_cast<size_t>(H) * 2);
+    w.total = off;
+    return w;
+}
+
+}  // namespace ksl
+
+extern "C" int ksl_moe_combine(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                               int64_t T, int64_t topk, int64_t H, void* y, int y_dtype,
+                               int64_t y_stride, void* stream) {
+    return ksl::launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
+    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+    return ksl::moe_workspace_layout(T, topk, E, H, I).total;
+}
+
+extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_stride,
+                                     const int64_t* topk_ids, const void* topk_w, int w_dtype,
+                                     const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z,
+                                     int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
+                                     void* y, int y_dtype, int64_t y_stride, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
+    if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (T == 0) return KSL_OK;
+    const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
+    if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return KSL_ERR_ALIGN;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* sorted_rows = reinterpret_cast<int32_t*>(ws + L.sorted_rows);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    int32_t* inv = reinterpret_cast<int32_t*>(ws + L.inv);
+    void* a16 = ws + L.a16;
+    void* out2 = ws + L.out2;
+    void* out3 = ws + L.out3;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
+                           hidden_stride, H, a16, st);
+    if (rc) return rc;
+    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st);
+    if (rc) return rc;
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    if (rc) return rc;
+    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+}
+
+extern "C" int ksl_version(void) { return 1; }
+
+extern "C" const char* ksl_status_string(int status) {
+    switch (status) {
+        case KSL_OK: return "ok";
+        case KSL_ERR_ARG: return "invalid argument (null pointer or unknown enum)";
+        case KSL_ERR_SHAPE: return "shape or divisibility contract violated";
+        case KSL_ERR_ALIGN: return "pointer or stride alignment contract violated";
+        case KSL_ERR_LAUNCH: return "kernel launch failed";
+        case KSL_ERR_WORKSPACE: return "workspace too small";
+    }
+    return "unknown status";
+}

@@ -1,0 +1,276 @@
+// Expert routing metadata on the GPU, plus the fp16 activation copy.
+//
+// Contract (kernels/fused_moe_w4.py:15-51, moe_align): expanded rows
+// i = t*topk + slot are sorted stably by expert id (ids clamped to <= E; E is
+// the dropped sentinel), each expert's run is padded to block_m, pad slots hold
+// Nexp = T*topk, expert_ids[b] names the expert owning block b (E past the
+// last block), and inv[i] is the sorted slot of row i (0 for dropped rows).
+//
+// One workgroup of 16 waves does the whole job in one launch:
+//   1. each wave owns a contiguous range of rows and counts its rows per
+//      expert in a private LDS row, 64 rows at a time: lanes holding the same
+//      expert find each other with ballots over the id bits, the lowest such
+//      lane adds the group size (no atomics);
+//   2. one thread per expert turns the 16 per-wave counts into per-wave bases
+//      (exclusive prefix over waves) and the expert total; a workgroup scan of
+//      the padded block counts gives each expert's first slot;
+//   3. each expert fills its own pad slots and block ids (disjoint writes);
+//   4. each wave replays its rows in order and scatters slot = expert start +
+//      wave base + rank among earlier equal lanes, so the order inside an
+//      expert is the original row order (stable).
+// Extra workgroups (blockIdx.x > 0) convert hidden to fp16 for the GEMMs,
+// storing every 8-element block in MFMA K-slot order {0,4,1,5,2,6,3,7}.
+#include "ksl_common.h"
+
+namespace ksl {
+namespace {
+
+constexpr int kRouteWaves = 16;
+constexpr int kRouteThreads = kRouteWaves * kWave;
+constexpr int kMaxExperts = 512;  // 16 waves x E int32 counters + E int64 starts fit in 64 KB of LDS
+constexpr int kPrepThreads = 256;
+
+__device__ __forceinline__ uint64_t match_key(int key, int nbits) {
+    uint64_t peers = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (key >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    return peers;
+}
+
+// Workgroup-wide exclusive scan of one int64 per thread (kRouteThreads threads).
+__device__ int64_t block_exclusive_scan(int64_t v, int64_t* lds_wave, int64_t* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int64_t incl = v;
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int64_t o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+    }
+    if (lane == kWave - 1) lds_wave[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        int64_t wv = lane < kRouteWaves ? lds_wave[lane] : 0;
+        int64_t wincl = wv;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int64_t o = __shfl_up(wincl, off, kWave);
+            if (lane >= off) wincl += o;
+        }
+        if (lane < kRouteWaves) lds_wave[lane] = wincl - wv;
+        if (lane == kRouteWaves - 1) *total = wincl;
+    }
+    __syncthreads();
+    return lds_wave[wave] + incl - v;
+}
+
+template <typename IdxT, int HD>
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(
+    const int64_t* __restrict__ ids, int64_t Nexp, int E, int64_t block_m,
+    IdxT* __restrict__ sorted_rows, int64_t cap, IdxT* __restrict__ expert_ids,
+    int64_t max_blocks, IdxT* __restrict__ inv, int32_t* __restrict__ offsets,
+    // fused activation prep (blockIdx.x > 0)
+    const void* __restrict__ hidden, int64_t hidden_stride, int64_t T, int64_t H,
+    f16* __restrict__ a16) {
+    if (blockIdx.x > 0) {
+        // ---- activation prep: hidden -> fp16, 8-blocks in K-slot order ----
+        typedef typename Elem<HD>::T HT;
+        const HT* h = static_cast<const HT*>(hidden);
+        const int64_t vec_per_row = H / 8;
+        const int64_t nvec = T * vec_per_row;
+        const int64_t nthreads = static_cast<int64_t>(gridDim.x - 1) * kRouteThreads;
+        for (int64_t v = static_cast<int64_t>(blockIdx.x - 1) * kRouteThreads + threadIdx.x; v < nvec;
+             v += nthreads) {
+            const int64_t t = v / vec_per_row;
+            const int64_t c0 = (v - t * vec_per_row) * 8;
+            float f[8];
+            load8<HD>(h + t * hidden_stride + c0, f);
+            f16x8 o;
+            o[0] = static_cast<f16>(f[0]);
+            o[1] = static_cast<f16>(f[4]);
+            o[2] = static_cast<f16>(f[1]);
+            o[3] = static_cast<f16>(f[5]);
+            o[4] = static_cast<f16>(f[2]);
+            o[5] = static_cast<f16>(f[6]);
+            o[6] = static_cast<f16>(f[3]);
+            o[7] = static_cast<f16>(f[7]);
+            *reinterpret_cast<f16x8*>(a16 + t * H + c0) = o;
+        }
+        return;
+    }
+
+    extern __shared__ int32_t lds[];
+    int32_t* wcnt = lds;                                  // [kRouteWaves][E]
+    int64_t* estart = reinterpret_cast<int64_t*>(lds + kRouteWaves * E);  // [E], 8-byte aligned (16*E ints)
+    int64_t* scan_tmp = estart + E;                       // [kRouteWaves]
+    int64_t* total_blocks = scan_tmp + kRouteWaves;       // [1]
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    int nbits = 1;
+    while ((1 << nbits) < E + 2) ++nbits;  // keys 0..E+1
+
+    for (int i = threadIdx.x; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
+    __syncthreads();
+
+    // rows owned by this wave: [r_begin, r_end), whole 64-row segments
+    const int64_t per_wave = ((Nexp + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
+    const int64_t r_begin = wave * per_wave;
+    const int64_t r_end = r_begin + per_wave < Nexp ? r_begin + per_wave : Nexp;
+    int32_t* mycnt = wcnt + wave * E;
+
+    // ---- 1. per-wave counts ----
+    for (int64_t base = r_begin; base < r_end; base += kWave) {
+        const int64_t r = base + lane;
+        int key = E + 1;  // not a row
+        if (r < r_end) {
+            const int64_t id = ids[r];
+            key = (id < 0 || id > E) ? E : static_cast<int>(id);
+        }
+        const uint64_t peers = match_key(key, nbits);
+        const bool leader = (__builtin_ctzll(peers) == lane);
+        if (leader && key < E) mycnt[key] += __builtin_popcountll(peers);
+    }
+    __syncthreads();
+
+    // ---- 2. per-wave bases, totals, expert starts ----
+    int64_t cnt = 0, nblk = 0;
+    const int e = threadIdx.x;
+    if (e < E) {
+        int32_t run = 0;
+        for (int w = 0; w < kRouteWaves; ++w) {
+            const int32_t c = wcnt[w * E + e];
+            wcnt[w * E + e] = run;
+            run += c;
+        }
+        cnt = run;
+        nblk = (cnt + block_m - 1) / block_m;
+    }
+    const int64_t blk_start = block_exclusive_scan(e < E ? nblk : 0, scan_tmp, total_blocks);
+    if (e < E) estart[e] = blk_start * block_m;
+    const int64_t tot_blocks = *total_blocks;
+
+    // ---- 3. pad slots, block ids, offsets (disjoint writes) ----
+    if (e < E) {
+        if (sorted_rows) {
+            for (int64_t p = blk_start * block_m + cnt; p < (blk_start + nblk) * block_m; ++p)
+                sorted_rows[p] = static_cast<IdxT>(Nexp);
+        }
+        if (expert_ids) {
+            for (int64_t b = blk_start; b < blk_start + nblk; ++b) expert_ids[b] = static_cast<IdxT>(e);
+        }
+        if (offsets) offsets[e] = static_cast<int32_t>(blk_start * block_m);
+    }
+    if (offsets && threadIdx.x == 0) offsets[E] = static_cast<int32_t>(tot_blocks * block_m);
+    if (sorted_rows) {
+        for (int64_t p = tot_blocks * block_m + threadIdx.x; p < cap; p += kRouteThreads)
+            sorted_rows[p] = static_cast<IdxT>(Nexp);
+    }
+    if (expert_ids) {
+        for (int64_t b = tot_blocks + threadIdx.x; b < max_blocks; b += kRouteThreads)
+            expert_ids[b] = static_cast<IdxT>(E);
+    }
+    __syncthreads();
+
+    // ---- 4. stable scatter ----
+    for (int64_t base = r_begin; base < r_end; base += kWave) {
+        const int64_t r = base + lane;
+        int key = E + 1;
+        if (r < r_end) {
+            const int64_t id = ids[r];
+            key = (id < 0 || id > E) ? E : static_cast<int>(id);
+        }
+        const uint64_t peers = match_key(key, nbits);
+        if (key < E) {
+            const int32_t before = mycnt[key];
+            const int64_t slot = estart[key] + before + __builtin_popcountll(peers & lt_mask);
+            if (sorted_rows) sorted_rows[slot] = static_cast<IdxT>(r);
+            if (inv) inv[r] = static_cast<IdxT>(slot);
+            if (__builtin_ctzll(peers) == lane) mycnt[key] = before + __builtin_popcountll(peers);
+        } else if (key == E) {
+            if (inv) inv[r] = 0;
+        }
+    }
+}
+
+template <typename IdxT, int HD>
+int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
+                 IdxT* sorted_rows, int64_t cap, IdxT* expert_ids, int64_t max_blocks, IdxT* inv,
+                 int32_t* offsets, const void* hidden, int64_t hstride, int64_t H, f16* a16,
+                 hipStream_t st) {
+    const int64_t Nexp = T * topk;
+    unsigned grid = 1;
+    if (a16) {
+        const int64_t nvec = T * (H / 8);
+        int64_t want = (nvec + kRouteThreads * 4 - 1) / (kRouteThreads * 4);
+        if (want < 1) want = 1;
+        if (want > 2048) want = 2048;
+        grid += static_cast<unsigned>(want);
+    }
+    const size_t lds_bytes = kRouteWaves * E * sizeof(int32_t) +
+                             (E + kRouteWaves + 1) * sizeof(int64_t);
+    hipLaunchKernelGGL((route_kernel<IdxT, HD>), dim3(grid), dim3(kRouteThreads), lds_bytes, st, ids,
+                       Nexp, static_cast<int>(E), block_m, sorted_rows, cap, expert_ids, max_blocks,
+                       inv, offsets, hidden, hstride, T, H, a16);
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+
+}  // namespace
+}  // namespace ksl
+
+extern "C" int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                             int64_t block_m, int64_t* sorted_rows, int64_t* expert_ids,
+                             int64_t* inv, void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts || block_m <= 0) return KSL_ERR_SHAPE;
+    if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    if (T > 0 && !topk_ids) return KSL_ERR_ARG;
+    const int64_t Nexp = T * topk;
+    const int64_t max_blocks = (Nexp + block_m - 1) / block_m + E;
+    const int64_t cap = max_blocks * block_m;
+    return launch_route<int64_t, KSL_DTYPE_BF16>(topk_ids, T, topk, E, block_m, sorted_rows, cap,
+                                                 expert_ids, max_blocks, inv, nullptr, nullptr, 0, 0,
+                                                 nullptr, static_cast<hipStream_t>(stream));
+}
+
+namespace ksl {
+int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
+                  int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
+                  int64_t H, void* a16, hipStream_t st) {
+    if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
+    if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    if (T > 0 && !ids) return KSL_ERR_ARG;
+    if (a16) {
+        if (!hidden || H <= 0 || H % 8 != 0 || hstride < H || hstride % 8 != 0) return KSL_ERR_SHAPE;
+        if (reinterpret_cast<uintptr_t>(hidden) % 16 || reinterpret_cast<uintptr_t>(a16) % 16)
+            return KSL_ERR_ALIGN;
+    }
+    const int64_t Nexp = T * topk;
+    f16* a = static_cast<f16*>(a16);
+    // compact layout: block_m = 1; slots past offsets[E] hold Nexp, only the
+    // first Nexp slots are materialised.
+    switch (hd) {
+        case KSL_DTYPE_BF16:
+            return launch_route<int32_t, KSL_DTYPE_BF16>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
+                                                         inv, offsets, hidden, hstride, H, a, st);
+        case KSL_DTYPE_F16:
+            return launch_route<int32_t, KSL_DTYPE_F16>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
+                                                        inv, offsets, hidden, hstride, H, a, st);
+        case KSL_DTYPE_F32:
+            return launch_route<int32_t, KSL_DTYPE_F32>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
+                                                        inv, offsets, hidden, hstride, H, a, st);
+    }
+    return KSL_ERR_ARG;
+}
+}  // namespace ksl
+
+extern "C" int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                             int32_t* sorted_rows, int32_t* offsets, int32_t* inv,
+                             const void* hidden, int hidden_dtype, int64_t hidden_stride, int64_t H,
+                             void* a16, void* stream) {
+    return ksl::route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
+                              hidden_stride, H, a16, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,155 @@
+"""W4A16 128-expert fused MoE forward on gfx950 — drop-in for kernels/fused_moe_w4_v2.py.
+
+  fused_moe_w4_v2(hidden, exp, topk_ids, topk_w) -> Tensor   (kernels/fused_moe_w4_v2.py:319-371)
+
+`exp` is the reference's duck-typed experts module (kernels/pack_experts.py:96-97):
+  gu_q uint8 [E, 2I, H/2], gu_s / gu_z fp16 [E, 2I, H/128]   (gate rows 0..I-1, up rows I..2I-1)
+  dn_q uint8 [E, H, I/2],  dn_s / dn_z fp16 [E, H, I/64]
+  act_fn                                                       (tanh-GELU or SiLU)
+Packed format (kernels/w4a16.py:19-48): byte j of a row = q[2j] | q[2j+1] << 4,
+W = fp16((q - zero) * scale) per (row, group).
+
+One C call launches four kernels on the current stream, with no host sync:
+routing metadata + fp16 activation copy, grouped gate/up GEMM with the
+activation in the epilogue, grouped down GEMM, fixed-order top-k combine.
+The combine is a fixed fp32 FMA chain over the top-k slots (no atomics), so
+the output is bit-identical run to run.
+
+Differences from the reference, on purpose:
+- SiLU-gated experts are supported next to tanh-GELU (the reference asserts
+  tanh-GELU, :291-308, :332).
+- The preshuffled down pack (MOE_NS, :180-245) is not used; `dn_ns` modules
+  are rejected.
+- zero-points must be integers in [0, 15] (what quantize_w4 writes,
+  kernels/w4a16.py:28); checked once per module.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_TANH_GELU_NAMES = ("gelu_pytorch_tanh", "gelu_new", "gelu_tanh", "quick_gelu_tanh")  # :291
+_SILU_NAMES = ("silu", "swish", "SiLU", "SiLUActivation")
+
+
+def hidden_device(exp):
+    """kernels/fused_moe_w4_v2.py:311-316."""
+    for b in ("gu_s", "gu_q"):
+        t = getattr(exp, b, None)
+        if t is not None:
+            return t.device
+    return "cpu"
+
+
+def _act_code(fn) -> int | None:
+    name = (getattr(fn, "__name__", None) or type(fn).__name__) if fn is not None else None
+    if name is None:
+        return None
+    if name in _TANH_GELU_NAMES or "gelu" in str(name).lower():
+        return _lib.ACT_GELU_TANH
+    if name in _SILU_NAMES or "silu" in str(name).lower() or "swish" in str(name).lower():
+        return _lib.ACT_SILU
+    # numeric probe (kernels/fused_moe_w4_v2.py:299-302), on the CPU
+    x = torch.tensor([-1.0, 0.0, 0.5, 2.0], dtype=torch.float32)
+    try:
+        out = fn(x).float()
+    except Exception:
+        return None
+    gelu = 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+    if torch.allclose(out, gelu, atol=1e-3):
+        return _lib.ACT_GELU_TANH
+    if torch.allclose(out, torch.nn.functional.silu(x), atol=1e-3):
+        return _lib.ACT_SILU
+    return None
+
+
+def _check_act(exp) -> bool:
+    """One-time guard (kernels/fused_moe_w4_v2.py:294-308): the epilogue is
+    tanh-GELU or SiLU; the module's act_fn must be one of them."""
+    fn = getattr(exp, "act_fn", None)
+    code = _act_code(fn)
+    name = (getattr(fn, "__name__", None) or type(fn).__name__) if fn is not None else None
+    assert code is not None, (
+        f"fused_moe_w4_v2 supports tanh-GELU and SiLU epilogues but this module's act_fn is {name!r}.")
+    exp._ksl_act = code
+    exp._act_checked = True
+    return True
+
+
+def _check_weights(exp, E, H, I) -> None:
+    if getattr(exp, "_ksl_weights_checked", False):
+        return
+    if getattr(exp, "dn_ns", False):
+        raise NotImplementedError("the preshuffled down pack (dn_ns) is not supported; keep dn_q as [E, H, I/2]")
+    spec = {
+        "gu_q": ((E, 2 * I, H // 2), torch.uint8),
+        "gu_s": ((E, 2 * I, H // 128), torch.float16),
+        "gu_z": ((E, 2 * I, H // 128), torch.float16),
+        "dn_q": ((E, H, I // 2), torch.uint8),
+        "dn_s": ((E, H, I // 64), torch.float16),
+        "dn_z": ((E, H, I // 64), torch.float16),
+    }
+    for name, (shape, dt) in spec.items():
+        t = getattr(exp, name)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"exp.{name} has shape {tuple(t.shape)}, expected {shape}")
+        if t.dtype != dt:
+            raise TypeError(f"exp.{name} has dtype {t.dtype}, expected {dt}")
+        if not t.is_contiguous():
+            raise ValueError(f"exp.{name} must be contiguous")
+        if not t.is_cuda:
+            raise ValueError(f"exp.{name} must be on the GPU")
+    for name in ("gu_z", "dn_z"):
+        z = getattr(exp, name)
+        ok = bool(((z == z.round()) & (z >= 0) & (z <= 15)).all().item())  # one sync, once per module
+        if not ok:
+            raise ValueError(f"exp.{name}: zero-points must be integers in [0, 15]")
+    exp._ksl_weights_checked = True
+
+
+def moe_workspace(T: int, tk: int, E: int, H: int, I: int, device) -> torch.Tensor:
+    nbytes = int(_lib.load().ksl_moe_workspace_bytes(T, tk, E, H, I))
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+@torch.no_grad()
+def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torch.Tensor,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+    T, K = hidden.shape
+    tk = topk_ids.shape[1]
+    E, twoI, _ = exp.gu_q.shape
+    I = twoI // 2
+    assert K % 128 == 0, f"hidden dim {K} must be divisible by 128 (gate_up group)"
+    assert I % 64 == 0, f"expert intermediate {I} must be divisible by 64 (down group)"
+    assert getattr(exp, "_act_checked", False) or _check_act(exp), "unsupported activation"
+    if not hasattr(exp, "_ksl_act"):
+        _check_act(exp)
+    _check_weights(exp, E, K, I)
+    if topk_ids.shape[0] != T or tuple(topk_w.shape) != (T, tk):
+        raise ValueError("topk_ids / topk_w must be [T, topk]")
+    dev = hidden.device
+    if hidden.stride(1) != 1 or hidden.stride(0) % 8 != 0 or hidden.data_ptr() % 16 != 0:
+        hidden = hidden.contiguous()
+    ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)
+    ids = ids.contiguous()
+    w = topk_w.contiguous()
+    out_dtype = hidden.dtype
+    # the reference stores fp16 for any non-bf16 hidden (:260-263)
+    y_dtype = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float16
+    y = torch.empty(T, K, dtype=y_dtype, device=dev)
+    if T == 0:
+        return y.to(out_dtype)
+    if workspace is None:
+        workspace = moe_workspace(T, tk, E, K, I, dev)
+    lib = _lib.load()
+    rc = lib.ksl_moe_w4a16_forward(
+        _lib.ptr(hidden), _lib.dtype_code(hidden.dtype), hidden.stride(0),
+        _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
+        _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z),
+        T, tk, E, K, I, exp._ksl_act,
+        _lib.ptr(y), _lib.dtype_code(y_dtype), y.stride(0),
+        _lib.ptr(workspace), workspace.numel(), _lib.stream_of(hidden))
+    _lib.check(rc, "ksl_moe_w4a16_forward")
+    return y if y_dtype == out_dtype else y.to(out_dtype)

@@ -1,0 +1,321 @@
+"""CPU restatement of the fused layer-kernel path (RMSNorm + W4A16 MoE), in numpy.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker: only tests/, the smoke()
+entry and the cpu_baseline leg of bench.py may import it. The product path
+(the HIP library behind the package) never calls into it.
+
+Every function restates the reference's arithmetic, with the reference
+file:line it follows. bf16 values travel as uint16 bit patterns (numpy has no
+bf16 type); fp16 values as numpy float16.
+
+Dtype chain restated (kernels/fused_moe_w4_v2.py:96-177, 248-263):
+  A      = fp16(hidden)                                  (:347)
+  W      = fp16((q - z) * s)  with q, z, s fp16          (:125-128, :172-175)
+  g, u   = A @ Wg^T, A @ Wu^T accumulated in fp32         (:128, :135)
+  out2   = fp16(act(g) * u), act evaluated in fp32       (:136-138)
+  out3   = fp16(out2 @ Wd^T) accumulated in fp32         (:175-177)
+  y[t]   = sum_k fp32(w[t,k]) * fp32(out3[inv[t*k+k']])  (:255-263), fixed k order
+The fp32 accumulations of the two GEMMs have no defined order in the
+reference (Triton tl.dot); this restatement accumulates in float64 and rounds
+once to fp32, which is the exact value any fp32 order approximates.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+GU_GS = 128  # kernels/pack_experts.py:12 (gate/up group size along K=H)
+DN_GS = 64   # kernels/pack_experts.py:12 (down group size along K=I)
+
+GELU_C0 = 0.7978845608028654  # sqrt(2/pi), kernels/fused_moe_w4_v2.py:136
+GELU_C1 = 0.044715            # kernels/fused_moe_w4_v2.py:136
+
+ACT_GELU_TANH = 0
+ACT_SILU = 1
+
+
+# ----------------------------------------------------------------------------
+# bf16 helpers (bit patterns in uint16)
+# ----------------------------------------------------------------------------
+def f32_to_bf16(x) -> np.ndarray:
+    """fp32 -> bf16 bits, round-to-nearest-even; NaN -> 0x7FC0 (torch's rule)."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r = np.where(nan, np.uint16(0x7FC0), r)
+    return r
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    b = np.asarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_to_bf16(x) -> np.ndarray:
+    return f32_to_bf16(np.asarray(x, dtype=np.float16).astype(np.float32))
+
+
+# ----------------------------------------------------------------------------
+# RMSNorm — kernels/fused_rmsnorm.py:10-21 (kernel), :24-32 (wrapper)
+# ----------------------------------------------------------------------------
+def rmsnorm(x32: np.ndarray, w32: np.ndarray | None, eps: float) -> np.ndarray:
+    """Returns bf16 bits of shape x32.shape.
+
+    x32: input already converted to fp32 (the kernel's `.to(tl.float32)`, :15).
+    ms = sum(x^2)/n + eps in fp32 (:16); the sum is taken exactly (float64)
+    and rounded once to fp32. y = x * (1/sqrt(ms)) (:17), then y * w (:19-20),
+    each step rounded to fp32, then stored as bf16 (:21).
+    """
+    x32 = np.asarray(x32, dtype=np.float32)
+    n = x32.shape[-1]
+    ss = np.sum(x32.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    ss32 = ss.astype(np.float32)
+    ms = (ss32 / np.float32(n)).astype(np.float32) + np.float32(eps)
+    ms = ms.astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(ms.astype(np.float64))).astype(np.float32)
+    y = (x32 * r).astype(np.float32)
+    if w32 is not None:
+        y = (y * np.asarray(w32, dtype=np.float32)).astype(np.float32)
+    return f32_to_bf16(y)
+
+
+# ----------------------------------------------------------------------------
+# W4 pack format — kernels/w4a16.py:19-48
+# ----------------------------------------------------------------------------
+def quantize_w4(W: np.ndarray, gs: int):
+    """W[N,K] float -> (q uint8[N,K/2], scale fp16[N,K/gs], zero fp16[N,K/gs]).
+
+    w4a16.py:22-32: per (row, group) scale=(max-min).clamp(1e-8)/15,
+    zero=round(-min/scale) clamped to [0,15], q=round(W/scale+zero) clamped;
+    byte j = q[2j] | q[2j+1] << 4 (low nibble = even k).
+    Rounding is round-half-to-even, as torch.round.
+    """
+    N, K = W.shape
+    assert K % gs == 0
+    Wg = W.astype(np.float32).reshape(N, K // gs, gs)
+    wmin = Wg.min(-1)
+    wmax = Wg.max(-1)
+    scale = (np.maximum(wmax - wmin, np.float32(1e-8)) / np.float32(15.0)).astype(np.float32)
+    zero = np.clip(np.round(-wmin / scale), 0, 15).astype(np.float32)
+    q = np.clip(np.round(Wg / scale[..., None] + zero[..., None]), 0, 15).astype(np.uint8)
+    q = q.reshape(N, K)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return packed, scale.astype(np.float16), zero.astype(np.float16)
+
+
+def unpack_nibbles(packed: np.ndarray) -> np.ndarray:
+    """uint8[..., K/2] -> uint8[..., K]; low nibble is the even k (w4a16.py:40-44)."""
+    lo = packed & 0xF
+    hi = packed >> 4
+    out = np.empty(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = lo
+    out[..., 1::2] = hi
+    return out
+
+
+def dequant_w4(packed: np.ndarray, scale: np.ndarray, zero: np.ndarray, gs: int) -> np.ndarray:
+    """fp16 weights W = fp16((q - z) * s) (w4a16.py:35-48 and the in-kernel
+    fp16 form fused_moe_w4_v2.py:125-128). (q - z) is an exact small integer
+    and (q - z) * s is exact in fp32, so one rounding to fp16 gives the
+    correctly rounded fp16 product, identical to both reference forms."""
+    q = unpack_nibbles(packed).astype(np.float32)
+    lead = q.shape[:-1]
+    K = q.shape[-1]
+    q = q.reshape(lead + (K // gs, gs))
+    W = (q - zero.astype(np.float32)[..., None]) * scale.astype(np.float32)[..., None]
+    return W.reshape(lead + (K,)).astype(np.float16)
+
+
+# ----------------------------------------------------------------------------
+# Routing metadata — kernels/fused_moe_w4.py:15-51 (moe_align)
+# ----------------------------------------------------------------------------
+def moe_align(topk_ids: np.ndarray, block_m: int, E: int):
+    """Returns (sorted_rows int64[cap], expert_ids int64[max_blocks], cap, inv int64[Nexp]).
+
+    fused_moe_w4.py:22 clamps ids to <= E (E = dropped sentinel); :25 stable
+    argsort by expert; :28-30 per-expert counts padded to block_m blocks;
+    :31-32 fixed capacity; :34 expert_ids = searchsorted(cum, b, right);
+    :35-39 sorted position = expert block start + rank within expert;
+    :43-50 pad slots hold Nexp, dropped rows map to inv 0.
+    """
+    topk_ids = np.asarray(topk_ids, dtype=np.int64)
+    T, tk = topk_ids.shape
+    flat = np.minimum(topk_ids.reshape(-1), E)
+    if (flat < 0).any():
+        raise IndexError("moe_align: negative expert id")
+    Nexp = flat.size
+    valid = flat < E
+    order = np.argsort(flat, kind="stable")
+    sorted_e = flat[order]
+    sv = sorted_e < E
+    counts = np.bincount(flat[valid], minlength=E)[:E].astype(np.int64)
+    nblk = (counts + block_m - 1) // block_m
+    max_blocks = (Nexp + block_m - 1) // block_m + E
+    cap = max_blocks * block_m
+    cum = np.cumsum(nblk)
+    expert_ids = np.searchsorted(cum, np.arange(max_blocks), side="right").astype(np.int64)
+    dst_start = (cum - nblk) * block_m
+    estart = np.cumsum(counts) - counts
+    se_c = np.minimum(sorted_e, E - 1)
+    pos = np.arange(Nexp) - estart[se_c]
+    dst = dst_start[se_c] + pos
+    sorted_rows = np.full(cap, Nexp, dtype=np.int64)
+    sorted_rows[dst[sv]] = order[sv]
+    inv = np.zeros(Nexp, dtype=np.int64)
+    inv[order[sv]] = dst[sv]
+    return sorted_rows, expert_ids, int(cap), inv
+
+
+# ----------------------------------------------------------------------------
+# Activations — kernels/fused_moe_w4_v2.py:136-138 (tanh-GELU), SiLU
+# ----------------------------------------------------------------------------
+def act_fp32(g: np.ndarray, act: int) -> np.ndarray:
+    g = g.astype(np.float32)
+    if act == ACT_GELU_TANH:
+        # 0.5*g*(1+tanh(c0*(g+c1*g^3))) with tanh = 2/(1+exp(-2*inner)) - 1
+        inner = np.float32(GELU_C0) * (g + np.float32(GELU_C1) * g * g * g)
+        with np.errstate(over="ignore"):
+            th = np.float32(2.0) / (np.float32(1.0) + np.exp(np.float32(-2.0) * inner)) - np.float32(1.0)
+        return (np.float32(0.5) * g * (np.float32(1.0) + th)).astype(np.float32)
+    if act == ACT_SILU:
+        with np.errstate(over="ignore"):
+            return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+    raise ValueError(f"unknown activation code {act}")
+
+
+def act_torch_semantics(g64: np.ndarray, act: int) -> np.ndarray:
+    """The stock activations (transformers GELUTanh / SiLU) in float64, used as
+    the mathematical check on act_fp32."""
+    if act == ACT_GELU_TANH:
+        return 0.5 * g64 * (1.0 + np.tanh(GELU_C0 * (g64 + GELU_C1 * g64 ** 3)))
+    return g64 / (1.0 + np.exp(-g64))
+
+
+# ----------------------------------------------------------------------------
+# Expert GEMMs — kernels/fused_moe_w4_v2.py:96-139 and :146-177
+# ----------------------------------------------------------------------------
+def _mm_f32(a16: np.ndarray, w16: np.ndarray) -> np.ndarray:
+    """fp16 x fp16^T with an exact (float64) accumulate rounded to fp32."""
+    return (a16.astype(np.float64) @ w16.astype(np.float64).T).astype(np.float32)
+
+
+def gateup_act(a16: np.ndarray, gu_w16: np.ndarray, act: int) -> np.ndarray:
+    """a16 fp16[M,H]; gu_w16 fp16[2I,H] (gate rows 0..I-1, up rows I..2I-1,
+    fused_moe_w4_v2.py:124, :130). Returns out2 fp16[M,I]."""
+    I = gu_w16.shape[0] // 2
+    g = _mm_f32(a16, gu_w16[:I])
+    u = _mm_f32(a16, gu_w16[I:])
+    return (act_fp32(g, act) * u).astype(np.float32).astype(np.float16)
+
+
+def down(out2: np.ndarray, dn_w16: np.ndarray) -> np.ndarray:
+    """out2 fp16[M,I]; dn_w16 fp16[H,I]. Returns out3 fp16[M,H] (:175-177)."""
+    return _mm_f32(out2, dn_w16).astype(np.float16)
+
+
+def combine_fma(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.ndarray:
+    """y[t] = fma-chain over k = 0..tk-1 of fp32(w[t,k]) * fp32(out3[inv[t*tk+k]])
+    starting from 0 (fused_moe_w4_v2.py:255-259), returned as fp32.
+    Each step is one fused multiply-add (Triton contracts `acc += w * x`),
+    emulated exactly: w*x is exact in float64 (24+11 bit mantissas) and the
+    sum with acc is rounded once to fp32 unless it needs more than 53 bits;
+    the C restatement (combine_c in oracle_c.c) uses fmaf and is the bit-exact
+    form."""
+    T, tk = topk_w.shape
+    acc = np.zeros((T, out3.shape[1]), dtype=np.float32)
+    w32 = topk_w.astype(np.float32)
+    for k in range(tk):
+        rows = out3[inv.reshape(T, tk)[:, k]].astype(np.float64)
+        acc = (acc.astype(np.float64) + w32[:, k:k + 1].astype(np.float64) * rows).astype(np.float32)
+    return acc
+
+
+def moe_forward(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
+                topk_ids: np.ndarray, topk_w: np.ndarray, act: int,
+                block_m: int = 32, return_parts: bool = False):
+    """One fused_moe_w4_v2 call (fused_moe_w4_v2.py:319-371), returning fp32
+    combine values (the caller rounds to hidden.dtype).
+
+    hidden_f32: the hidden values (bf16 or fp16) already widened to fp32.
+    """
+    T, H = hidden_f32.shape
+    E, twoI, _ = gu_q.shape
+    I = twoI // 2
+    tk = topk_ids.shape[1]
+    assert H % 128 == 0 and I % 64 == 0
+    Nexp = T * tk
+    sorted_rows, expert_ids, cap, inv = moe_align(topk_ids, block_m, E)
+    a16 = hidden_f32.astype(np.float16)                      # :347 hidden.to(fp16)
+    out2 = np.zeros((cap, I), dtype=np.float16)
+    out3 = np.zeros((cap, H), dtype=np.float16)
+    nblk = expert_ids.shape[0]
+    for b in range(nblk):
+        e = int(expert_ids[b])
+        if e >= E:
+            continue
+        rows = sorted_rows[b * block_m:(b + 1) * block_m]
+        valid = rows < Nexp
+        if not valid.any():
+            continue
+        idx = np.nonzero(valid)[0] + b * block_m
+        toks = rows[valid] // tk
+        gu_w16 = dequant_w4(gu_q[e], gu_s[e], gu_z[e], GU_GS)
+        out2[idx] = gateup_act(a16[toks], gu_w16, act)
+        dn_w16 = dequant_w4(dn_q[e], dn_s[e], dn_z[e], DN_GS)
+        out3[idx] = down(out2[idx], dn_w16)
+    y = combine_fma(out3, inv, topk_w)
+    if return_parts:
+        return y, dict(sorted_rows=sorted_rows, expert_ids=expert_ids, cap=cap, inv=inv,
+                       out2=out2, out3=out3)
+    return y
+
+
+def moe_forward_per_expert(hidden_f32, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
+                           topk_ids, topk_w, act):
+    """Same values as moe_forward, organised per expert (compact rows, the
+    layout the GPU path uses). Returns (y fp32 [T,H], per-expanded-row out3
+    fp16 [T*tk, H]). Rows routed to the dropped sentinel E get zeros."""
+    T, H = hidden_f32.shape
+    E, twoI, _ = gu_q.shape
+    I = twoI // 2
+    tk = topk_ids.shape[1]
+    flat = np.minimum(np.asarray(topk_ids, dtype=np.int64).reshape(-1), E)
+    a16 = hidden_f32.astype(np.float16)
+    out3_rows = np.zeros((T * tk, H), dtype=np.float16)
+    out2_rows = np.zeros((T * tk, I), dtype=np.float16)
+    for e in range(E):
+        r = np.nonzero(flat == e)[0]
+        if r.size == 0:
+            continue
+        gu_w16 = dequant_w4(gu_q[e], gu_s[e], gu_z[e], GU_GS)
+        dn_w16 = dequant_w4(dn_q[e], dn_s[e], dn_z[e], DN_GS)
+        o2 = gateup_act(a16[r // tk], gu_w16, act)
+        out2_rows[r] = o2
+        out3_rows[r] = down(o2, dn_w16)
+    # combine over compact rows: inv = identity on expanded rows
+    inv = np.arange(T * tk)
+    valid_any = (flat < E)
+    if not valid_any.all():
+        # reference: dropped rows map to sorted position 0 (the first valid row)
+        first = np.nonzero(valid_any)[0]
+        if first.size:
+            order = np.argsort(flat, kind="stable")
+            inv = np.where(valid_any, inv, order[0])
+    y = combine_fma(out3_rows, inv, topk_w)
+    return y, out2_rows, out3_rows
+
+
+# ----------------------------------------------------------------------------
+# Synthetic inputs (the workload definitions) — torch CPU generators so CPU and
+# GPU see identical bits.
+# ----------------------------------------------------------------------------
+def route_softmax_topk(logits: np.ndarray, k: int):
+    """softmax(fp32) -> top-k -> renormalise (TF modeling_diffusion_gemma.py:538-547,
+    per_expert_scale = 1). Uses torch.topk on CPU for its tie order."""
+    import torch
+    lg = torch.from_numpy(np.ascontiguousarray(logits, dtype=np.float32))
+    p = torch.softmax(lg, dim=-1, dtype=torch.float32)
+    w, idx = torch.topk(p, k=k, dim=-1)
+    w = w / w.sum(dim=-1, keepdim=True)
+    return idx.numpy().astype(np.int64), w.numpy().astype(np.float32)
