@@ -207,10 +207,10 @@ extern "C" int ksl_rmsnorm(const void* x, int x_dtype, const void* w, int w_dtyp
                            int y_dtype, int64_t rows, int64_t cols, int64_t x_stride,
                            int64_t y_stride, float eps, void* stream) {
     using namespace ksl;
-    if (!x || !y) return KSL_ERR_ARG;
     if (rows < 0 || cols <= 0 || x_stride < cols || y_stride < cols) return KSL_ERR_SHAPE;
     if (cols > (1 << 30) || rows > (int64_t(1) << 40)) return KSL_ERR_SHAPE;
     if (rows == 0) return KSL_OK;
+    if (!x || !y) return KSL_ERR_ARG;
     if (!w) w_dtype = KSL_DTYPE_BF16;
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (x_dtype) {
