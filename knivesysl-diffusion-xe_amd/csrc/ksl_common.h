@@ -107,6 +107,18 @@ template <> __device__ __forceinline__ void store8<KSL_DTYPE_F32>(void* p, const
 // word is {0,4,1,5,2,6,3,7}; activations are stored in the same order.
 // zc = 1024 + zero (exact for integer zero-points in [0, 15]); the result is
 // q - zero, exact in fp16.
+// fp16((q - zero) * scale) for the 8 nibbles of w, in K-slot order: the
+// reference's dequantised weight (kernels/w4a16.py:47-48), exact: (q - zero)
+// is an exact small integer and the product is rounded once to fp16.
+__device__ __forceinline__ f16x8 nib8_dequant(uint32_t w, f16x2 zc, f16x2 sc) {
+    const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
+    f16x2 h0 = (__builtin_bit_cast(f16x2, (w & m) | magic) - zc) * sc;
+    f16x2 h1 = (__builtin_bit_cast(f16x2, ((w >> 4) & m) | magic) - zc) * sc;
+    f16x2 h2 = (__builtin_bit_cast(f16x2, ((w >> 8) & m) | magic) - zc) * sc;
+    f16x2 h3 = (__builtin_bit_cast(f16x2, ((w >> 12) & m) | magic) - zc) * sc;
+    return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
 __device__ __forceinline__ f16x8 nib8_minus_zero(uint32_t w, f16x2 zc) {
     const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
     f16x2 h0 = __builtin_bit_cast(f16x2, (w & m) | magic) - zc;
