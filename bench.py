@@ -11,10 +11,11 @@ A "step" is one layer. Consecutive steps rotate over independent weight sets
 (3 x 412 MB by default) so the 256 MB MALL cannot serve weights from cache.
 
 Timed passes (all inside this process, same stream):
-  1. value: K steps of the layer (two C calls per step: RMSNorm, fused MoE
-     forward), bracketed by synchronize; µs per layer = elapsed / K.
+  1. value: K steps of the layer (one C call per step, four launches:
+     routing + RMSNorm + fp16 activations, gate/up, down, combine), bracketed
+     by synchronize; µs per layer = elapsed / K.
   2. per-kernel: K steps issued stage by stage with HIP events between the
-     five launches; the average duration of each kernel, from which the
+     four launches; the average duration of each kernel, from which the
      dominant kernel's achieved bandwidth (roofline) is computed.
   3. cpu_baseline: the reference CPU path (torch eager, oracle/cpu_baseline.py)
      on the host cores, bounded to ~20 s.
@@ -102,7 +103,6 @@ def main() -> int:
     runner = layer_mod.LayerRunner(T, TOPK, E, H, I, dev)
     ws = torch.empty(int(L.ksl_moe_workspace_bytes(T, TOPK, E, H, I)), dtype=torch.uint8, device=dev)
     y = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    xn = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     p = lib.ptr
     st = lib.stream_of(xg)
     v2 = importlib.import_module(f"{PKG}.fused_moe_w4_v2")
@@ -111,16 +111,14 @@ def main() -> int:
         v2._check_weights(exp, E, H, I)
 
     def step(exp):
-        rc = L.ksl_rmsnorm(p(xg), lib.DTYPE_BF16, p(nwg), lib.DTYPE_BF16, p(xn), lib.DTYPE_BF16, T, H, H, H,
-                           1e-6, st)
-        if rc:
-            lib.check(rc, "ksl_rmsnorm")
-        rc = L.ksl_moe_w4a16_forward(p(xn), lib.DTYPE_BF16, H, p(idsg), p(wg), lib.DTYPE_F32,
+        # one C call: routing + RMSNorm + fp16 activations, gate/up, down, combine
+        rc = L.ksl_moe_layer_forward(p(xg), lib.DTYPE_BF16, H, p(nwg), lib.DTYPE_BF16, 1e-6,
+                                     p(idsg), p(wg), lib.DTYPE_F32,
                                      p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z),
                                      T, TOPK, E, H, I, exp._ksl_act, p(y), lib.DTYPE_BF16, H,
                                      p(ws), ws.numel(), st)
         if rc:
-            lib.check(rc, "ksl_moe_w4a16_forward")
+            lib.check(rc, "ksl_moe_layer_forward")
 
     # ---- pass 1: whole-layer time -------------------------------------------
     for i in range(args.warmup):

@@ -89,6 +89,31 @@ int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_s
                           void* y, int y_dtype, int64_t y_stride,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* RMSNorm followed by the W4A16 MoE forward: the layer as the experts see it
+ * (DiffusionGemma decoder layer, TF modeling_diffusion_gemma.py:731-733:
+ * experts(pre_feedforward_layernorm_2(x), topk_ids, topk_w)), four launches.
+ * The norm (kernels/fused_rmsnorm.py:10-21 semantics; norm_w may be NULL) is
+ * fused with the routing and the fp16 activation copy (ksl_moe_layer_route);
+ * then gate/up, down and combine as in ksl_moe_w4a16_forward. x: bf16 or fp16
+ * [T, H], row stride x_stride; H <= 4096. The normalised activations are
+ * consumed in fp16 (bf16 norm output -> fp16, as hidden.to(fp16) does in
+ * kernels/fused_moe_w4_v2.py:347). Same workspace as ksl_moe_w4a16_forward.
+ * Not a reference entry point: the reference runs the two as separate calls. */
+int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
+                          int norm_w_dtype, float eps, const int64_t* topk_ids, const void* topk_w,
+                          int w_dtype, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
+                          int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
+                          int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The first launch of ksl_moe_layer_forward: compact routing (as
+ * ksl_moe_route) plus a16 = fp16(bf16(rmsnorm(x) [* norm_w])) in the gate/up
+ * activation order, one launch. */
+int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                        int32_t* sorted_rows, int32_t* offsets, int32_t* inv, const void* x, int x_dtype,
+                        int64_t x_stride, const void* norm_w, int norm_w_dtype, float eps, int64_t H,
+                        void* a16, void* stream);
+
 /* ---- the forward's stages, exposed for tests and for callers that fuse
  *      their own pipeline (same kernels as ksl_moe_w4a16_forward) ---------- */
 
@@ -96,8 +121,9 @@ int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_s
  * sorted slots [offsets[e], offsets[e+1]); sorted_rows int32[T*topk] (tail
  * past offsets[E] = T*topk); inv int32[T*topk]. Plus, in the same launch, the
  * fp16 activation copy a16[T, H] (hidden.to(fp16), fused_moe_w4_v2.py:347)
- * stored with each 8-element block in MFMA K-slot order {0,4,1,5,2,6,3,7}.
- * a16 may be NULL (routing only). */
+ * in the gate/up activation order: within each 128-element group, logical
+ * offset c*32 + i*8 + j is stored at i*32 + c*8 + s(j), s the inverse of the
+ * MFMA K-slot order {0,4,1,5,2,6,3,7}. a16 may be NULL (routing only). */
 int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
                   int32_t* sorted_rows, int32_t* offsets, int32_t* inv,
                   const void* hidden, int hidden_dtype, int64_t hidden_stride, int64_t H,
@@ -105,7 +131,9 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
 
 /* Grouped W4 gate/up GEMM with the activation fused in the epilogue.
  * Replaces _gateup_act_kernel (kernels/fused_moe_w4_v2.py:96-139).
- * out2 fp16 [T*topk, I] row per sorted slot, 8-blocks in K-slot order. */
+ * out2 fp16 [T*topk, I] row per sorted slot, in the down activation order:
+ * within each 64-element group, offset c*16 + i*8 + j is stored at
+ * i*32 + c*8 + s(j). */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
                        int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);

@@ -101,30 +101,56 @@ template <> __device__ __forceinline__ void store8<KSL_DTYPE_F32>(void* p, const
 
 // ---- W4 nibble decode -------------------------------------------------------
 // A 32-bit word of the packed format holds k0..k7 of one weight row, k_i in
-// bits [4i, 4i+4) (byte j = q[2j] | q[2j+1] << 4). OR-ing a nibble into the
-// mantissa of fp16 1024.0 (0x6400) gives exactly 1024 + q. The four pairs come
-// out as (k0,k4), (k1,k5), (k2,k6), (k3,k7), so the MFMA K-slot order of one
-// word is {0,4,1,5,2,6,3,7}; activations are stored in the same order.
-// zc = 1024 + zero (exact for integer zero-points in [0, 15]); the result is
-// q - zero, exact in fp16.
-// fp16((q - zero) * scale) for the 8 nibbles of w, in K-slot order: the
-// reference's dequantised weight (kernels/w4a16.py:47-48), exact: (q - zero)
-// is an exact small integer and the product is rounded once to fp16.
-__device__ __forceinline__ f16x8 nib8_dequant(uint32_t w, f16x2 zc, f16x2 sc) {
-    const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
-    f16x2 h0 = (__builtin_bit_cast(f16x2, (w & m) | magic) - zc) * sc;
-    f16x2 h1 = (__builtin_bit_cast(f16x2, ((w >> 4) & m) | magic) - zc) * sc;
-    f16x2 h2 = (__builtin_bit_cast(f16x2, ((w >> 8) & m) | magic) - zc) * sc;
-    f16x2 h3 = (__builtin_bit_cast(f16x2, ((w >> 12) & m) | magic) - zc) * sc;
+// bits [4i, 4i+4) (byte j = q[2j] | q[2j+1] << 4). Each fp16 pair is built by
+// one AND-OR into the mantissa of a power of two:
+//   (w      & 0x000F000F) | 0x6400 6400 = (1024 + k0, 1024 + k4)   ulp 1
+//   (w      & 0x00F000F0) | 0x5400 5400 = (  64 + k1,   64 + k5)   ulp 1/16
+//   (w >> 8 & 0x000F000F) | 0x6400 6400 = (1024 + k2, 1024 + k6)
+//   (w >> 8 & 0x00F000F0) | 0x5400 5400 = (  64 + k3,   64 + k7)
+// so one word is 1 shift + 4 AND-ORs, and its MFMA K-slot order is
+// {0,4,1,5,2,6,3,7}; activations are stored in the same order. Subtracting
+// (1024 + zero) resp. (64 + zero) leaves q - zero, exact in fp16 for integer
+// zero-points in [0, 15].
+struct NibConsts {
+    uint32_t m_lo, m_hi, b_lo, b_hi;
+};
+
+// The constants are laundered through empty asm so that the selector keeps
+// them in registers and emits v_and_or_b32 (gfx9 VOP3 takes no literal).
+__device__ __forceinline__ NibConsts nib_consts() {
+    NibConsts c{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+    asm volatile("" : "+s"(c.m_lo), "+s"(c.m_hi));
+    asm volatile("" : "+v"(c.b_lo), "+v"(c.b_hi));
+    return c;
+}
+
+// Zero-point pairs for one weight row: (1024 + z, 1024 + z) and (64 + z, 64 + z).
+struct ZeroPair {
+    f16x2 lo, hi;
+};
+__device__ __forceinline__ ZeroPair zero_pair(f16 z) {
+    const f16 a = z + static_cast<f16>(1024.0f), b = z + static_cast<f16>(64.0f);
+    return ZeroPair{f16x2{a, a}, f16x2{b, b}};
+}
+
+__device__ __forceinline__ f16x8 nib8_minus_zero(uint32_t w, const ZeroPair& zc, const NibConsts& k) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = __builtin_bit_cast(f16x2, (w & k.m_lo) | k.b_lo) - zc.lo;
+    const f16x2 h1 = __builtin_bit_cast(f16x2, (w & k.m_hi) | k.b_hi) - zc.hi;
+    const f16x2 h2 = __builtin_bit_cast(f16x2, (w8 & k.m_lo) | k.b_lo) - zc.lo;
+    const f16x2 h3 = __builtin_bit_cast(f16x2, (w8 & k.m_hi) | k.b_hi) - zc.hi;
     return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
-__device__ __forceinline__ f16x8 nib8_minus_zero(uint32_t w, f16x2 zc) {
-    const uint32_t m = 0x000F000Fu, magic = 0x64006400u;
-    f16x2 h0 = __builtin_bit_cast(f16x2, (w & m) | magic) - zc;
-    f16x2 h1 = __builtin_bit_cast(f16x2, ((w >> 4) & m) | magic) - zc;
-    f16x2 h2 = __builtin_bit_cast(f16x2, ((w >> 8) & m) | magic) - zc;
-    f16x2 h3 = __builtin_bit_cast(f16x2, ((w >> 12) & m) | magic) - zc;
+// fp16((q - zero) * scale) for the 8 nibbles of w, in K-slot order: the
+// reference's dequantised weight (kernels/w4a16.py:47-48), exact: (q - zero)
+// is an exact small integer and the product is rounded once to fp16.
+__device__ __forceinline__ f16x8 nib8_dequant(uint32_t w, const ZeroPair& zc, f16x2 sc, const NibConsts& k) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = (__builtin_bit_cast(f16x2, (w & k.m_lo) | k.b_lo) - zc.lo) * sc;
+    const f16x2 h1 = (__builtin_bit_cast(f16x2, (w & k.m_hi) | k.b_hi) - zc.hi) * sc;
+    const f16x2 h2 = (__builtin_bit_cast(f16x2, (w8 & k.m_lo) | k.b_lo) - zc.lo) * sc;
+    const f16x2 h3 = (__builtin_bit_cast(f16x2, (w8 & k.m_hi) | k.b_hi) - zc.hi) * sc;
     return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
@@ -134,8 +160,64 @@ __device__ __forceinline__ int perm8_store_index(int n) {
     return (n & ~7) | (o < 4 ? 2 * o : 2 * (o - 4) + 1);
 }
 
+// Activation storage order of the expert GEMMs. Within one quantisation group
+// of GS elements (GS = 128 for gate/up over H, 64 for down over I), MFMA step
+// i (GS/32 steps) of lane group c (4 groups) covers logical offsets
+// c*(GS/4) + i*8 .. +8. Those 8-element chunks are stored step-major at
+// i*32 + c*8, so one fragment block (fixed i, all 16 rows x 4 lane groups)
+// reads 64 contiguous bytes per row; inside a chunk the K-slot order is
+// {0,4,1,5,2,6,3,7}. Returns the storage index of logical column n.
+template <int GS>
+__device__ __forceinline__ int act_store_index(int n) {
+    constexpr int Q = GS / 4;  // logical span of one lane group
+    const int g0 = n & ~(GS - 1), o = n & (GS - 1);
+    const int c = o / Q, i = (o % Q) >> 3;
+    return g0 + i * 32 + c * 8 + (perm8_store_index(o) & 7);
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// ---- RMSNorm of one row, shared by the standalone kernel and the fused layer
+// prep (kernels/fused_rmsnorm.py:10-21). The row is split over LPR = 1 << lpr_log2
+// lanes; lane sl owns 8 consecutive columns per step, NSTEP steps, so
+// c0(s) = s*8*LPR + sl*8. x and w are loaded up front (one round trip), the
+// fp32 sum of squares is reduced over the LPR lanes by a fixed xor tree, and
+// out[s][j] receives bf16(x * (1/sqrt(ms)) [* w]) as a float.
+template <int XD, int WD, int NSTEP, bool HAS_W>
+__device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__ xr,
+                                        const typename Elem<WD>::T* __restrict__ w, int cols, float eps,
+                                        int sl, int lpr_log2, bool row_ok, float (&out)[NSTEP][8]) {
+    const int stride_cols = 8 << lpr_log2;
+    float wf[NSTEP][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+        const int c0 = s * stride_cols + sl * 8;
+        if (row_ok && c0 < cols) {
+            load8<XD>(xr + c0, out[s]);
+            if (HAS_W) load8<WD>(w + c0, wf[s]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out[s][j] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(out[s][j], out[s][j], ss);
+    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    const float ms = ss / static_cast<float>(cols) + eps;
+    const float r = 1.0f / __builtin_sqrtf(ms);
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float o = out[s][j] * r;
+            if (HAS_W) o = o * wf[s][j];
+            out[s][j] = bf16_bits_to_f32(f32_to_bf16_bits(o));  // the reference stores bf16
+        }
 }
 
 }  // namespace ksl

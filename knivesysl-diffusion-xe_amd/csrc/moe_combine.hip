@@ -12,6 +12,9 @@ namespace ksl {
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
                   int64_t H, void* a16, hipStream_t st);
+int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
+               int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
+               int wd, float eps, int64_t H, void* a16, hipStream_t st);
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
                   int64_t I, int act, void* out2, hipStream_t st);
@@ -40,12 +43,27 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    for (int k = 0; k < topk; ++k) {
-        const int64_t r = inv[t * topk + k];
-        const float wk = Elem<WD>::load(w + t * topk + k);
-        const f16x8 x = *reinterpret_cast<const f16x8*>(out3 + r * H + c0);
+    // 8 slots at a time: all index/weight loads, then all row loads (clamped slot
+    // index: one round trip each), then the FMA chain in slot order.
+    for (int k0 = 0; k0 < topk; k0 += 8) {
+        int32_t r[8];
+        float wk[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wk, static_cast<float>(x[j]), acc[j]);
+        for (int k = 0; k < 8; ++k) {
+            const int kk = k0 + k < topk ? k0 + k : topk - 1;
+            r[k] = inv[t * topk + kk];
+            wk[k] = Elem<WD>::load(w + t * topk + kk);
+        }
+        f16x8 x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = *reinterpret_cast<const f16x8*>(out3 + static_cast<int64_t>(r[k]) * H + c0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (k0 + k < topk) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wk[k], static_cast<float>(x[k][j]), acc[j]);
+            }
+        }
     }
     store8<YD>(y + t * ys + c0, acc);
 }
@@ -161,6 +179,48 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+}
+
+extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
+                                     int norm_w_dtype, float eps, const int64_t* topk_ids,
+                                     const void* topk_w, int w_dtype, const uint8_t* gu_q,
+                                     const void* gu_s, const void* gu_z, const uint8_t* dn_q,
+                                     const void* dn_s, const void* dn_z, int64_t T, int64_t topk,
+                                     int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
+                                     int64_t y_stride, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
+    if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (T == 0) return KSL_OK;
+    const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
+    if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return KSL_ERR_ALIGN;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* sorted_rows = reinterpret_cast<int32_t*>(ws + L.sorted_rows);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    int32_t* inv = reinterpret_cast<int32_t*>(ws + L.inv);
+    void* a16 = ws + L.a16;
+    void* out2 = ws + L.out2;
+    void* out3 = ws + L.out3;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
+                        norm_w_dtype, eps, H, a16, st);
+    if (rc) return rc;
+    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st);
+    if (rc) return rc;
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    if (rc) return rc;
+    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+}
+
+extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                                   int32_t* sorted_rows, int32_t* offsets, int32_t* inv, const void* x,
+                                   int x_dtype, int64_t x_stride, const void* norm_w, int norm_w_dtype,
+                                   float eps, int64_t H, void* a16, void* stream) {
+    return ksl::route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
+                           norm_w_dtype, eps, H, a16, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ksl_version(void) { return 1; }

@@ -64,15 +64,24 @@ __device__ __forceinline__ float act_times_up(float g, float u) {
 }
 
 // ---------------------------------------------------------------- gate / up
-constexpr int kGuWaves = 4;                   // each wave: one gate tile + one up tile
-constexpr int kGuWgCols = 16 * kGuWaves;      // 64 columns of I per workgroup
-constexpr int kGuThreads = kGuWaves * kWave;  // 256
-constexpr int kGuSlab = 2;                    // quantisation groups (2 x 128 K) per A slab
-constexpr int kGuPD = 2 * kGuSlab;            // weight groups in flight per wave
-constexpr int kMaxMt = 2;                     // 16-row M tiles per row chunk
-constexpr int kGuSlabBytes = kMaxMt * kGuSlab * 4 * kWave * 16;  // 16 KB per slab buffer
-constexpr int kGuMaxG = 32;                   // H <= 4096
-constexpr int kGuSzPer = 4 * 32 * kGuMaxG / kGuThreads;  // scale/zero dwords per thread (max)
+// Producer / consumer workgroup: 4 consumer waves (each one gate tile and one
+// up tile of 16 columns of I) and 4 producer waves. Producers only issue
+// global loads - the workgroup's weights and gathered activations for one
+// quantisation group (128 K) at a time - keep kGuLead groups in flight in
+// their registers, and write each arrived group into a two-slot LDS ring.
+// Consumers only read LDS, decode and run MFMA; they never wait on memory
+// counters. One barrier per group hands a slot from producers to consumers.
+constexpr int kGuCons = 4;                       // consumer waves
+constexpr int kGuProd = 4;                       // producer waves
+constexpr int kGuWgCols = 16 * kGuCons;          // 64 columns of I per workgroup
+constexpr int kGuThreads = (kGuCons + kGuProd) * kWave;  // 512
+constexpr int kGuLead = 4;                       // groups of loads in flight per producer
+constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
+constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
+constexpr int kGuSlotW = 2 * kGuCons * kBlk;     // 8 KB of weights per group
+constexpr int kGuSlot = kGuSlotW + kMaxMt * 4 * kBlk;  // + 8 KB of activations
+constexpr int kGuMaxG = 32;                      // H <= 4096
+constexpr int kGuSzPer = 4 * 32 * kGuMaxG / (kGuProd * kWave);  // scale/zero dwords per producer lane
 
 struct GuArgs {
     const f16* a16;
@@ -85,183 +94,127 @@ struct GuArgs {
     int topk, I, H;
 };
 
-// Per-wave state for one (expert, column block) tile.
-struct GuWave {
-    const uint8_t* wq0;  // gate row of this lane, + c*16 bytes
-    const uint8_t* wq1;  // up row
-    int n0;              // first column of I of this wave
-};
+// Producer wave p (0..3) loads, per group: the gate and up fragment blocks of
+// consumer wave p (lane L = c*16 + col: row col of the tile, bytes c*16.. of
+// the group's 64) and the activation blocks (t, i = p) for t < MT (lane L:
+// row t*16 + L%16, stored chunk g*128 + p*32 + (L/16)*8: 64 contiguous bytes
+// per row, see act_store_index).
+template <int MT>
+struct GuProducer {
+    const uint8_t* wq0;   // gate row, + c*16
+    const uint8_t* wq1;   // up row
+    const f16* ar[MT];    // activation row (gathered token), + c*32 + p*8
+    u32x4 v[kGuLead][2 + MT];
 
-// Scale/zero dwords of the workgroup's 64 gate and 64 up rows, four [64 x G]
-// fp16 blocks (s_gate, z_gate, s_up, z_up), loaded into registers first and
-// written to LDS with the first activation slab.
-struct GuSz {
-    uint32_t v[kGuSzPer];
+    __device__ __forceinline__ void load(int g, u32x4 (&dst)[2 + MT]) const {
+        dst[0] = *reinterpret_cast<const u32x4*>(wq0 + g * 64);
+        dst[1] = *reinterpret_cast<const u32x4*>(wq1 + g * 64);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) dst[2 + t] = *reinterpret_cast<const u32x4*>(ar[t] + g * 128);
+    }
+    __device__ __forceinline__ void store(char* slot, int p, int lane, const u32x4 (&src)[2 + MT]) const {
+        *reinterpret_cast<u32x4*>(slot + (p * 2 + 0) * kBlk + lane * 16) = src[0];
+        *reinterpret_cast<u32x4*>(slot + (p * 2 + 1) * kBlk + lane * 16) = src[1];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            *reinterpret_cast<u32x4*>(slot + kGuSlotW + (t * 4 + p) * kBlk + lane * 16) = src[2 + t];
+    }
 };
 
 template <int ACT, int MT>
-__device__ __forceinline__ void gateup_chunk(const GuArgs& A, const GuWave& W, char* __restrict__ lds_a,
-                                             f16* __restrict__ lds_sz, const GuSz& sz, bool store_sz,
-                                             int start, int m0, int mrows) {
+__device__ __forceinline__ void gateup_chunk(const GuArgs& A, int e, int nb, char* __restrict__ lds,
+                                             const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
     const int tid = threadIdx.x;
+    const int wave = tid / kWave;
     const int lane = tid & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
     const int G = A.H >> 7;
-    const int NS = (G + kGuSlab - 1) / kGuSlab;
+    const int Gp = (G + kGuLead - 1) / kGuLead * kGuLead;  // groups padded to whole load rounds
+    char* slot0 = lds;
+
+    if (wave >= kGuCons) {
+        // ------------------------------------------------------------ producer
+        const int p = wave - kGuCons;
+        GuProducer<MT> P;
+        const int64_t rg = static_cast<int64_t>(e) * 2 * A.I + nb * kGuWgCols + p * 16 + col;
+        P.wq0 = A.gu_q + rg * (A.H >> 1) + c * 16;
+        P.wq1 = A.gu_q + (rg + A.I) * (A.H >> 1) + c * 16;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            int r = t * 16 + col;
+            if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
+            const int tok = A.sorted_rows[start + m0 + r] / A.topk;
+            P.ar[t] = A.a16 + static_cast<int64_t>(tok) * A.H + p * 32 + c * 8;
+        }
+        // prologue: groups 0..kGuLead-1 in flight, group 0 into slot 0
+#pragma unroll
+        for (int u = 0; u < kGuLead; ++u) P.load(u < G ? u : G - 1, P.v[u]);
+        P.store(slot0, p, lane, P.v[0]);
+        __syncthreads();
+        // step i: group i+1 (set (i+1)%L) -> slot (i+1)%2; loads of group i+L -> set i%L
+        for (int g0 = 0; g0 < Gp; g0 += kGuLead) {
+#pragma unroll
+            for (int u = 0; u < kGuLead; ++u) {
+                const int i = g0 + u;
+                P.store(slot0 + ((i + 1) & 1) * kGuSlot, p, lane, P.v[(u + 1) % kGuLead]);
+                const int gl = i + kGuLead < G ? i + kGuLead : G - 1;
+                P.load(gl, P.v[u]);
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // -------------------------------------------------------------- consumer
+    const NibConsts kn = nib_consts();
     const f16* sg = lds_sz;
     const f16* zg = lds_sz + 64 * G;
     const f16* su = lds_sz + 2 * 64 * G;
     const f16* zu = lds_sz + 3 * 64 * G;
-    const int wcol = (tid / kWave) * 16 + col;  // row of this lane within the workgroup's 64
-
-    // Staging of A slabs: chunk ch = tid + 256*j (j < 2*MT) covers row r = ch/32 and
-    // the 16-byte K chunk kc = ch%32 of the slab (K offset kc*8 within 256).
-    constexpr int NCH = 2 * MT;
-    const f16* src[NCH];
-    int dst[NCH];
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-        const int ch = tid + kGuThreads * j;
-        int r = ch >> 5;
-        const int kc = ch & 31;
-        const int rr = r & 15, t = r >> 4;
-        const int gs = kc >> 4, cc = (kc >> 2) & 3, i = kc & 3;
-        dst[j] = (((t * kGuSlab + gs) * 4 + i) * kWave + cc * 16 + rr) * 16;
-        if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
-        const int tok = A.sorted_rows[start + m0 + r] / A.topk;
-        src[j] = A.a16 + static_cast<int64_t>(tok) * A.H + kc * 8;
-    }
-    // Every global load below is unconditional (addresses clamped instead):
-    // a load under a branch makes the wait-count pass drain all loads in flight.
-    auto stage_load = [&](int s, u32x4 (&stg)[NCH]) {
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-            const int kc8 = ((tid + kGuThreads * j) & 31) * 8;
-            // past H (odd G, last slab): reload the slab start; feeds only groups >= G
-            const int soff = s * 256 + kc8 < A.H ? s * 256 : -kc8;
-            stg[j] = *reinterpret_cast<const u32x4*>(src[j] + soff);
-        }
-    };
-    auto stage_store = [&](int buf, const u32x4 (&stg)[NCH]) {
-#pragma unroll
-        for (int j = 0; j < NCH; ++j)
-            *reinterpret_cast<u32x4*>(lds_a + buf * kGuSlabBytes + dst[j]) = stg[j];
-    };
-
+    const int wcol = wave * 16 + col;  // row of this lane within the workgroup's 64
     f32x4 acc[2][MT];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    u32x4 wb[kGuPD][2];
-    u32x4 stg[NCH];
-    stage_load(0, stg);  // before the weight prefetch: waiting for it waits for nothing else
+    __syncthreads();  // slot 0 and the scale table are ready
+    for (int i = 0; i < Gp; ++i) {
+        if (i < G) {
+            const char* slot = slot0 + (i & 1) * kGuSlot;
+            const u32x4 w0 = *reinterpret_cast<const u32x4*>(slot + (wave * 2 + 0) * kBlk + lane * 16);
+            const u32x4 w1 = *reinterpret_cast<const u32x4*>(slot + (wave * 2 + 1) * kBlk + lane * 16);
+            const float s0 = static_cast<float>(sg[wcol * G + i]);
+            const float s1 = static_cast<float>(su[wcol * G + i]);
+            const ZeroPair zc0 = zero_pair(zg[wcol * G + i]);
+            const ZeroPair zc1 = zero_pair(zu[wcol * G + i]);
+            f32x4 part[2][MT];
 #pragma unroll
-    for (int p = 0; p < kGuPD; ++p) {
-        const int gp = p < G ? p : G - 1;
-        wb[p][0] = *reinterpret_cast<const u32x4*>(W.wq0 + gp * 64);
-        wb[p][1] = *reinterpret_cast<const u32x4*>(W.wq1 + gp * 64);
-    }
-    if (store_sz) {
-        const int nd = 4 * 32 * G;
-        uint32_t* d = reinterpret_cast<uint32_t*>(lds_sz);
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int k = 0; k < kGuSzPer; ++k) {
-            const int i = tid + k * kGuThreads;
-            if (i < nd) d[i] = sz.v[k];
-        }
-    }
-    stage_store(0, stg);
-    __syncthreads();
-
-    // One quantisation group g, activations from LDS buffer P, weights from
-    // prefetch slot SLOT (both compile-time); afterwards the slot is refilled
-    // with group g + kGuPD (clamped: a redundant cached load, never a branch).
-    auto group = [&](int g, auto GSc, auto Pc, auto SLOTc) {
-        constexpr int gs = decltype(GSc)::value;
-        constexpr int P = decltype(Pc)::value;
-        constexpr int SLOT = decltype(SLOTc)::value;
-        const u32x4 w0 = wb[SLOT][0], w1 = wb[SLOT][1];
-        const float s0 = static_cast<float>(sg[wcol * G + g]);
-        const float s1 = static_cast<float>(su[wcol * G + g]);
-        const f16 z0 = zg[wcol * G + g] + static_cast<f16>(1024.0f);
-        const f16 z1 = zu[wcol * G + g] + static_cast<f16>(1024.0f);
-        const f16x2 zc0{z0, z0}, zc1{z1, z1};
-        f32x4 part[2][MT];
+                for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int k = 0; k < 4; ++k) {
+                const f16x8 b0 = nib8_minus_zero(w0[k], zc0, kn);
+                const f16x8 b1 = nib8_minus_zero(w1[k], zc1, kn);
 #pragma unroll
-            for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f16x8 b0 = nib8_minus_zero(w0[i], zc0);
-            const f16x8 b1 = nib8_minus_zero(w1[i], zc1);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(
-                    lds_a + P * kGuSlabBytes + (((t * kGuSlab + gs) * 4 + i) * kWave + lane) * 16);
-                part[0][t] = mfma16x16x32(a, b0, part[0][t]);
-                part[1][t] = mfma16x16x32(a, b1, part[1][t]);
+                for (int t = 0; t < MT; ++t) {
+                    const f16x8 a = *reinterpret_cast<const f16x8*>(slot + kGuSlotW + (t * 4 + k) * kBlk + lane * 16);
+                    part[0][t] = mfma16x16x32(a, b0, part[0][t]);
+                    part[1][t] = mfma16x16x32(a, b1, part[1][t]);
+                }
             }
-        }
-        {
-            const int gn = g + kGuPD < G ? g + kGuPD : G - 1;
-            wb[SLOT][0] = *reinterpret_cast<const u32x4*>(W.wq0 + gn * 64);
-            wb[SLOT][1] = *reinterpret_cast<const u32x4*>(W.wq1 + gn * 64);
-        }
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
+            for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc[0][t][r] = __builtin_fmaf(s0, part[0][t][r], acc[0][t][r]);
-                acc[1][t][r] = __builtin_fmaf(s1, part[1][t][r], acc[1][t][r]);
-            }
-        __builtin_amdgcn_sched_barrier(0);  // bound live ranges to one group
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    // The next slab's activation loads go out before the slab's weight prefetches.
-    auto next_slab_load = [&](int s) {
-        stage_load(s < NS ? s : NS - 1, stg);
-        __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the slab's weight prefetches
-    };
-
-    // Steady state: two slabs (four groups) per iteration, no branches inside.
-    int g = 0;
-    for (; g + 4 <= G; g += 4) {
-        const int s = g / kGuSlab;
-        next_slab_load(s + 1);
-        group(g, I0{}, I0{}, I0{});
-        group(g + 1, I1{}, I0{}, I1{});
-        stage_store(1, stg);
-        __syncthreads();
-        next_slab_load(s + 2);
-        group(g + 2, I0{}, I1{}, I2{});
-        group(g + 3, I1{}, I1{}, I3{});
-        stage_store(0, stg);
+                for (int r = 0; r < 4; ++r) {
+                    acc[0][t][r] = __builtin_fmaf(s0, part[0][t][r], acc[0][t][r]);
+                    acc[1][t][r] = __builtin_fmaf(s1, part[1][t][r], acc[1][t][r]);
+                }
+        }
         __syncthreads();
     }
-    // Tail of G % 4 groups (buffer 0 holds slab g/2, prefetch slots 0.. hold them).
-    const int rem = G - g;
-    if (rem == 1) {
-        group(g, I0{}, I0{}, I0{});
-    } else if (rem == 2) {
-        group(g, I0{}, I0{}, I0{});
-        group(g + 1, I1{}, I0{}, I1{});
-    } else if (rem == 3) {
-        next_slab_load(g / kGuSlab + 1);
-        group(g, I0{}, I0{}, I0{});
-        group(g + 1, I1{}, I0{}, I1{});
-        stage_store(1, stg);
-        __syncthreads();
-        group(g + 2, I0{}, I1{}, I2{});
-    }
-    __syncthreads();  // LDS slab buffers free for the next chunk
-
-    const int sc = perm8_store_index(W.n0 + col);
+    const int n0 = nb * kGuWgCols + wave * 16;
+    const int sc = act_store_index<64>(n0 + col);  // out2 is the down GEMM's activation
     f16* o = A.out2 + static_cast<int64_t>(start + m0) * A.I + sc;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -274,7 +227,7 @@ __device__ __forceinline__ void gateup_chunk(const GuArgs& A, const GuWave& W, c
 }
 
 template <int ACT>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2))) void gateup_act_kernel(GuArgs A) {
+__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(4))) void gateup_act_kernel(GuArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int nb_per_e = A.I / kGuWgCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -286,38 +239,38 @@ __global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(2)))
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
-    const int lane = tid & (kWave - 1);
-    const int col = lane & 15, c = lane >> 4;
-
-    char* lds_a = lds;
-    f16* lds_sz = reinterpret_cast<f16*>(lds + 2 * kGuSlabBytes);
-    // scales / zeros: loads issued first, stored to LDS by the first chunk
-    GuSz sz;
-    {
+    f16* lds_sz = reinterpret_cast<f16*>(lds + 2 * kGuSlot);
+    // scales / zeros of the 64 gate and 64 up rows: four [64 x G] fp16 blocks
+    // (s_gate, z_gate, s_up, z_up), copied by the producers; published by the
+    // first barrier of the first chunk.
+    if (wave >= kGuCons) {
+        const int pt = tid - kGuCons * kWave;
         const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + nb * kGuWgCols;
         const int64_t up0 = gate0 + A.I;
-        const int nd = 32 * G;  // dwords per [64 x G] block (block starts are 4-byte aligned)
+        const int nd = 32 * G;  // dwords per block (block starts are 4-byte aligned)
+        uint32_t v[kGuSzPer];
 #pragma unroll
         for (int k = 0; k < kGuSzPer; ++k) {
-            int i = tid + k * kGuThreads;
+            int i = pt + k * kGuProd * kWave;
             if (i >= 4 * nd) i = 0;  // clamped, never stored
             const int b = i / nd, o = i - b * nd;
             const f16* base = ((b & 1) ? A.gu_z : A.gu_s) + ((b & 2) ? up0 : gate0) * G;
-            sz.v[k] = reinterpret_cast<const uint32_t*>(base)[o];
+            v[k] = reinterpret_cast<const uint32_t*>(base)[o];
+        }
+        uint32_t* d = reinterpret_cast<uint32_t*>(lds_sz);
+#pragma unroll
+        for (int k = 0; k < kGuSzPer; ++k) {
+            const int i = pt + k * kGuProd * kWave;
+            if (i < 4 * nd) d[i] = v[k];
         }
     }
-    GuWave W;
-    W.n0 = nb * kGuWgCols + wave * 16;
-    const int64_t rg = static_cast<int64_t>(e) * 2 * A.I + W.n0 + col;
-    W.wq0 = A.gu_q + rg * (A.H >> 1) + c * 16;
-    W.wq1 = A.gu_q + (rg + A.I) * (A.H >> 1) + c * 16;
-    // the first chunk's barrier (after its slab 0 staging) also publishes lds_sz
     for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
         const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
         if (mrows <= 16)
-            gateup_chunk<ACT, 1>(A, W, lds_a, lds_sz, sz, m0 == 0, start, m0, mrows);
+            gateup_chunk<ACT, 1>(A, e, nb, lds, lds_sz, start, m0, mrows);
         else
-            gateup_chunk<ACT, 2>(A, W, lds_a, lds_sz, sz, m0 == 0, start, m0, mrows);
+            gateup_chunk<ACT, 2>(A, e, nb, lds, lds_sz, start, m0, mrows);
+        __syncthreads();  // ring free for the next chunk
     }
 }
 
@@ -349,7 +302,8 @@ __device__ __forceinline__ void dma16(const void* src, char* lds_block) {
 }
 
 // The activation rows of one chunk, A[g][t][i] blocks: block (g, t, i) holds,
-// for lane L = c*16 + rr, out2[row t*16 + rr][g*64 + c*16 + i*8 .. +8].
+// for lane L = c*16 + rr, logical out2[row t*16 + rr][g*64 + c*16 + i*8 .. +8],
+// stored at g*64 + i*32 + c*8 (act_store_index<64>).
 template <int G>
 __device__ __forceinline__ void down_stage_a(const DnArgs& A, char* lds_a, int start, int m0, int mrows,
                                              int mt) {
@@ -363,7 +317,7 @@ __device__ __forceinline__ void down_stage_a(const DnArgs& A, char* lds_a, int s
         const int g = (b >> 1) / mt;
         int r = t * 16 + rr;
         if (r >= mrows) r = mrows - 1;
-        const f16* src = A.out2 + static_cast<int64_t>(start + m0 + r) * A.I + g * 64 + c * 16 + i * 8;
+        const f16* src = A.out2 + static_cast<int64_t>(start + m0 + r) * A.I + g * 64 + i * 32 + c * 8;
         dma16(src, lds_a + ((g * kMaxMt + t) * 2 + i) * kDnBlock);
     }
 }
@@ -377,6 +331,7 @@ __device__ __forceinline__ void down_chunk(const DnArgs& A, const u32x2 (&w)[kDn
     // B operand, b = fp16((q - z) * s), the reference's own dequantised weight.
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
+    const NibConsts kn = nib_consts();
     f32x4 acc[kDnTiles][MT];
 #pragma unroll
     for (int j = 0; j < kDnTiles; ++j)
@@ -384,14 +339,14 @@ __device__ __forceinline__ void down_chunk(const DnArgs& A, const u32x2 (&w)[kDn
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        f16x2 sc[kDnTiles], zc[kDnTiles];
+        f16x2 sc[kDnTiles];
+        ZeroPair zc[kDnTiles];
 #pragma unroll
         for (int j = 0; j < kDnTiles; ++j) {
             const int r = wrow0 + j * 16 + col;
             const f16 sv = lds_s[r * G + g];
-            const f16 z = lds_z[r * G + g] + static_cast<f16>(1024.0f);
             sc[j] = f16x2{sv, sv};
-            zc[j] = f16x2{z, z};
+            zc[j] = zero_pair(lds_z[r * G + g]);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -401,7 +356,7 @@ __device__ __forceinline__ void down_chunk(const DnArgs& A, const u32x2 (&w)[kDn
                 a[t] = *reinterpret_cast<const f16x8*>(lds_a + ((g * kMaxMt + t) * 2 + i) * kDnBlock + lane * 16);
 #pragma unroll
             for (int j = 0; j < kDnTiles; ++j) {
-                const f16x8 b = nib8_dequant(w[j][g][i], zc[j], sc[j]);
+                const f16x8 b = nib8_dequant(w[j][g][i], zc[j], sc[j], kn);
 #pragma unroll
                 for (int t = 0; t < MT; ++t) acc[j][t] = mfma16x16x32(a[t], b, acc[j][t]);
             }
@@ -534,7 +489,7 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     A.I = static_cast<int>(I);
     A.H = static_cast<int>(H);
     const unsigned grid = static_cast<unsigned>(E * (I / kGuWgCols));
-    const size_t lds = 2 * kGuSlabBytes + 4 * 64 * (H / 128) * sizeof(f16);
+    const size_t lds = 2 * kGuSlot + 4 * 64 * (H / 128) * sizeof(f16);
     if (act == KSL_ACT_GELU_TANH)
         hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH>), dim3(grid), dim3(kGuThreads), lds, st, A);
     else if (act == KSL_ACT_SILU)

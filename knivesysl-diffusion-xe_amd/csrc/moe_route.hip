@@ -19,7 +19,7 @@
 //      wave base + rank among earlier equal lanes, so the order inside an
 //      expert is the original row order (stable).
 // Extra workgroups (blockIdx.x > 0) convert hidden to fp16 for the GEMMs,
-// storing every 8-element block in MFMA K-slot order {0,4,1,5,2,6,3,7}.
+// in the gate/up activation order (act_store_index<128>).
 #include "ksl_common.h"
 
 namespace ksl {
@@ -27,6 +27,7 @@ namespace {
 
 constexpr int kRouteWaves = 16;
 constexpr int kRouteThreads = kRouteWaves * kWave;
+constexpr int kRouteSeg = 4;  // 64-row segments per wave per key batch
 constexpr int kMaxExperts = 512;  // 16 waves x E int32 counters + E int64 starts fit in 64 KB of LDS
 constexpr int kPrepThreads = 256;
 
@@ -65,11 +66,20 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* lds_wave, int64_t* t
     return lds_wave[wave] + incl - v;
 }
 
+struct RouteOut {
+    int64_t Nexp, cap, max_blocks, block_m;
+    int E;
+};
+
+template <typename IdxT>
+__device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, IdxT* __restrict__ sorted_rows,
+                           IdxT* __restrict__ expert_ids, IdxT* __restrict__ inv,
+                           int32_t* __restrict__ offsets);
+
 template <typename IdxT, int HD>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
-    const int64_t* __restrict__ ids, int64_t Nexp, int E, int64_t block_m,
-    IdxT* __restrict__ sorted_rows, int64_t cap, IdxT* __restrict__ expert_ids,
-    int64_t max_blocks, IdxT* __restrict__ inv, int32_t* __restrict__ offsets,
+    const int64_t* __restrict__ ids, RouteOut R, IdxT* __restrict__ sorted_rows,
+    IdxT* __restrict__ expert_ids, IdxT* __restrict__ inv, int32_t* __restrict__ offsets,
     // fused activation prep (blockIdx.x > 0)
     const void* __restrict__ hidden, int64_t hidden_stride, int64_t T, int64_t H,
     f16* __restrict__ a16) {
@@ -95,11 +105,61 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
             o[5] = static_cast<f16>(f[6]);
             o[6] = static_cast<f16>(f[3]);
             o[7] = static_cast<f16>(f[7]);
-            *reinterpret_cast<f16x8*>(a16 + t * H + c0) = o;
+            *reinterpret_cast<f16x8*>(a16 + t * H + act_store_index<128>(static_cast<int>(c0))) = o;
         }
         return;
     }
+    route_block<IdxT>(ids, R, sorted_rows, expert_ids, inv, offsets);
+}
 
+// RMSNorm of each token row fused with the activation prep: one wave per row
+// (64 lanes x 8 columns x NSTEP), the bf16-rounded norm output converted to
+// fp16 in the gate/up activation order. Workgroup 0 builds the routing.
+template <int XD, int WD, int NSTEP, bool HAS_W>
+__global__ __launch_bounds__(kRouteThreads) void route_norm_kernel(
+    const int64_t* __restrict__ ids, RouteOut R, int32_t* __restrict__ sorted_rows,
+    int32_t* __restrict__ inv, int32_t* __restrict__ offsets, const void* __restrict__ xv,
+    int64_t x_stride, const void* __restrict__ wv, float eps, int64_t T, int64_t H,
+    f16* __restrict__ a16) {
+    if (blockIdx.x == 0) {
+        route_block<int32_t>(ids, R, sorted_rows, nullptr, inv, offsets);
+        return;
+    }
+    typedef typename Elem<XD>::T XT;
+    typedef typename Elem<WD>::T WT;
+    const XT* x = static_cast<const XT*>(xv);
+    const WT* w = static_cast<const WT*>(wv);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t nworkers = static_cast<int64_t>(gridDim.x - 1) * kRouteWaves;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x - 1) * kRouteWaves + wave; row < T; row += nworkers) {
+        float v[NSTEP][8];
+        rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true, v);
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) {
+            const int c0 = s * 512 + lane * 8;
+            if (c0 < H) {
+                f16x8 o;
+                o[0] = static_cast<f16>(v[s][0]);
+                o[1] = static_cast<f16>(v[s][4]);
+                o[2] = static_cast<f16>(v[s][1]);
+                o[3] = static_cast<f16>(v[s][5]);
+                o[4] = static_cast<f16>(v[s][2]);
+                o[5] = static_cast<f16>(v[s][6]);
+                o[6] = static_cast<f16>(v[s][3]);
+                o[7] = static_cast<f16>(v[s][7]);
+                *reinterpret_cast<f16x8*>(a16 + row * H + act_store_index<128>(c0)) = o;
+            }
+        }
+    }
+}
+
+template <typename IdxT>
+__device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, IdxT* __restrict__ sorted_rows,
+                           IdxT* __restrict__ expert_ids, IdxT* __restrict__ inv,
+                           int32_t* __restrict__ offsets) {
+    const int64_t Nexp = R.Nexp, cap = R.cap, max_blocks = R.max_blocks, block_m = R.block_m;
+    const int E = R.E;
     extern __shared__ int32_t lds[];
     int32_t* wcnt = lds;                                  // [kRouteWaves][E]
     int64_t* estart = reinterpret_cast<int64_t*>(lds + kRouteWaves * E);  // [E], 8-byte aligned (16*E ints)
@@ -121,17 +181,35 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const int64_t r_end = r_begin + per_wave < Nexp ? r_begin + per_wave : Nexp;
     int32_t* mycnt = wcnt + wave * E;
 
-    // ---- 1. per-wave counts ----
-    for (int64_t base = r_begin; base < r_end; base += kWave) {
-        const int64_t r = base + lane;
-        int key = E + 1;  // not a row
-        if (r < r_end) {
-            const int64_t id = ids[r];
-            key = (id < 0 || id > E) ? E : static_cast<int>(id);
+    // Keys of this wave's rows, kRouteSeg 64-row segments at a time: all loads of
+    // a batch go out together (clamped indices, one round trip); with at most
+    // kRouteSeg segments per wave (T * topk <= 4096) the keys stay in registers
+    // for the scatter phase.
+    const int64_t nrows = r_end > r_begin ? r_end - r_begin : 0;
+    const int nseg = static_cast<int>((nrows + kWave - 1) / kWave);
+    int keys[kRouteSeg];
+    auto load_keys = [&](int seg0) {
+#pragma unroll
+        for (int s = 0; s < kRouteSeg; ++s) {
+            const int64_t r = r_begin + static_cast<int64_t>(seg0 + s) * kWave + lane;
+            const bool ok = r < r_end;
+            const int64_t id = ids[ok ? r : 0];
+            keys[s] = !ok ? E + 1 : ((id < 0 || id > E) ? E : static_cast<int>(id));  // E + 1: not a row
         }
-        const uint64_t peers = match_key(key, nbits);
-        const bool leader = (__builtin_ctzll(peers) == lane);
-        if (leader && key < E) mycnt[key] += __builtin_popcountll(peers);
+    };
+
+    // ---- 1. per-wave counts ----
+    for (int seg0 = 0; seg0 < nseg; seg0 += kRouteSeg) {
+        load_keys(seg0);
+#pragma unroll
+        for (int s = 0; s < kRouteSeg; ++s) {
+            if (seg0 + s < nseg) {
+                const int key = keys[s];
+                const uint64_t peers = match_key(key, nbits);
+                const bool leader = (__builtin_ctzll(peers) == lane);
+                if (leader && key < E) mycnt[key] += __builtin_popcountll(peers);
+            }
+        }
     }
     __syncthreads();
 
@@ -175,24 +253,30 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     __syncthreads();
 
     // ---- 4. stable scatter ----
-    for (int64_t base = r_begin; base < r_end; base += kWave) {
-        const int64_t r = base + lane;
-        int key = E + 1;
-        if (r < r_end) {
-            const int64_t id = ids[r];
-            key = (id < 0 || id > E) ? E : static_cast<int>(id);
-        }
-        const uint64_t peers = match_key(key, nbits);
-        if (key < E) {
-            const int32_t before = mycnt[key];
-            const int64_t slot = estart[key] + before + __builtin_popcountll(peers & lt_mask);
-            if (sorted_rows) sorted_rows[slot] = static_cast<IdxT>(r);
-            if (inv) inv[r] = static_cast<IdxT>(slot);
-            if (__builtin_ctzll(peers) == lane) mycnt[key] = before + __builtin_popcountll(peers);
-        } else if (key == E) {
-            if (inv) inv[r] = 0;
+    for (int seg0 = 0; seg0 < nseg; seg0 += kRouteSeg) {
+        if (nseg > kRouteSeg) load_keys(seg0);  // else the keys are still in registers
+#pragma unroll
+        for (int s = 0; s < kRouteSeg; ++s) {
+            if (seg0 + s < nseg) {
+                const int64_t r = r_begin + static_cast<int64_t>(seg0 + s) * kWave + lane;
+                const int key = keys[s];
+                const uint64_t peers = match_key(key, nbits);
+                if (key < E) {
+                    const int32_t before = mycnt[key];
+                    const int64_t slot = estart[key] + before + __builtin_popcountll(peers & lt_mask);
+                    if (sorted_rows) sorted_rows[slot] = static_cast<IdxT>(r);
+                    if (inv) inv[r] = static_cast<IdxT>(slot);
+                    if (__builtin_ctzll(peers) == lane) mycnt[key] = before + __builtin_popcountll(peers);
+                } else if (key == E) {
+                    if (inv) inv[r] = 0;
+                }
+            }
         }
     }
+}
+
+size_t route_lds_bytes(int64_t E) {
+    return kRouteWaves * E * sizeof(int32_t) + (E + kRouteWaves + 1) * sizeof(int64_t);
 }
 
 template <typename IdxT, int HD>
@@ -209,11 +293,10 @@ int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t
         if (want > 2048) want = 2048;
         grid += static_cast<unsigned>(want);
     }
-    const size_t lds_bytes = kRouteWaves * E * sizeof(int32_t) +
-                             (E + kRouteWaves + 1) * sizeof(int64_t);
-    hipLaunchKernelGGL((route_kernel<IdxT, HD>), dim3(grid), dim3(kRouteThreads), lds_bytes, st, ids,
-                       Nexp, static_cast<int>(E), block_m, sorted_rows, cap, expert_ids, max_blocks,
-                       inv, offsets, hidden, hstride, T, H, a16);
+    const size_t lds_bytes = route_lds_bytes(E);
+    RouteOut R{Nexp, cap, max_blocks, block_m, static_cast<int>(E)};
+    hipLaunchKernelGGL((route_kernel<IdxT, HD>), dim3(grid), dim3(kRouteThreads), lds_bytes, st, ids, R,
+                       sorted_rows, expert_ids, inv, offsets, hidden, hstride, T, H, a16);
     KSL_LAUNCH_CHECK();
     return KSL_OK;
 }
@@ -262,6 +345,66 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
         case KSL_DTYPE_F32:
             return launch_route<int32_t, KSL_DTYPE_F32>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
                                                         inv, offsets, hidden, hstride, H, a, st);
+    }
+    return KSL_ERR_ARG;
+}
+}  // namespace ksl
+
+namespace ksl {
+namespace {
+template <int XD, int WD, bool HAS_W>
+int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32_t* sorted_rows, int32_t* inv,
+                         int32_t* offsets, const void* x, int64_t xs, const void* w, float eps, int64_t T,
+                         int64_t H, f16* a16, hipStream_t st) {
+    int64_t want = (T + kRouteWaves - 1) / kRouteWaves;
+    if (want < 1) want = 1;
+    if (want > 4096) want = 4096;
+    const unsigned grid = 1 + static_cast<unsigned>(want);
+    const size_t lds = route_lds_bytes(R.E);
+#define KSL_RN(NS)                                                                                         \
+    hipLaunchKernelGGL((route_norm_kernel<XD, WD, NS, HAS_W>), dim3(grid), dim3(kRouteThreads), lds, st, ids, R, \
+                       sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16)
+    if (nstep <= 1) KSL_RN(1);
+    else if (nstep <= 2) KSL_RN(2);
+    else if (nstep <= 4) KSL_RN(4);
+    else if (nstep <= 6) KSL_RN(6);
+    else KSL_RN(8);
+#undef KSL_RN
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+template <int XD>
+int launch_route_norm_x(int wd, int nstep, const int64_t* ids, const RouteOut& R, int32_t* sorted_rows, int32_t* inv,
+                        int32_t* offsets, const void* x, int64_t xs, const void* w, float eps, int64_t T,
+                        int64_t H, f16* a16, hipStream_t st) {
+    if (!w) return launch_route_norm_ns<XD, KSL_DTYPE_BF16, false>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+    switch (wd) {
+        case KSL_DTYPE_BF16: return launch_route_norm_ns<XD, KSL_DTYPE_BF16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+        case KSL_DTYPE_F16: return launch_route_norm_ns<XD, KSL_DTYPE_F16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+        case KSL_DTYPE_F32: return launch_route_norm_ns<XD, KSL_DTYPE_F32, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+    }
+    return KSL_ERR_ARG;
+}
+}  // namespace
+
+// Routing plus RMSNorm -> fp16 activations in one launch (the layer path).
+int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
+               int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
+               int wd, float eps, int64_t H, void* a16, hipStream_t st) {
+    if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
+    if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    if (H <= 0 || H % 128 != 0 || H > 4096 || xs < H || xs % 8 != 0) return KSL_ERR_SHAPE;
+    if (T > 0 && (!ids || !x || !a16)) return KSL_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(a16) % 16 ||
+        (w && reinterpret_cast<uintptr_t>(w) % 16))
+        return KSL_ERR_ALIGN;
+    const int64_t Nexp = T * topk;
+    RouteOut R{Nexp, Nexp, 0, 1, static_cast<int>(E)};
+    const int nstep = static_cast<int>((H / 8 + kWave - 1) / kWave);
+    f16* a = static_cast<f16*>(a16);
+    switch (xd) {
+        case KSL_DTYPE_BF16: return launch_route_norm_x<KSL_DTYPE_BF16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, st);
+        case KSL_DTYPE_F16: return launch_route_norm_x<KSL_DTYPE_F16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, st);
     }
     return KSL_ERR_ARG;
 }

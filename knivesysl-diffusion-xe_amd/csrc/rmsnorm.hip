@@ -40,67 +40,45 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_vec_kernel(
     const bool row_ok = row < rows;
     const int stride_cols = 8 * lpr;
 
-    float v[NSTEP > 0 ? NSTEP : 1][8];
-    float ss = 0.0f;
-    const XT* xr = x + (row_ok ? row : 0) * xs;
+    constexpr int NS1 = NSTEP > 0 ? NSTEP : 1;
     if (NSTEP > 0) {
+        float v[NS1][8];
+        rms_row<XD, WD, NS1, HAS_W>(x + (row_ok ? row : 0) * xs, w, cols, eps, sl, lpr_log2, row_ok, v);
+        if (!row_ok) return;
+        YT* yr = y + row * ys;
 #pragma unroll
-        for (int s = 0; s < NSTEP; ++s) {
+        for (int s = 0; s < NS1; ++s) {
             const int c0 = s * stride_cols + sl * 8;
-            if (row_ok && c0 < cols) {
-                load8<XD>(xr + c0, v[s]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[s][j] = 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(v[s][j], v[s][j], ss);
+            if (c0 < cols) store8<YD>(yr + c0, v[s]);
         }
-    } else {
-        for (int c0 = sl * 8; c0 < cols; c0 += stride_cols) {
-            if (!row_ok) break;
-            float t[8];
-            load8<XD>(xr + c0, t);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(t[j], t[j], ss);
-        }
+        return;
     }
-    // xor-tree reduction inside the LPR-lane group (fixed order).
+    // long rows: two passes over x
+    const XT* xr = x + (row_ok ? row : 0) * xs;
+    float ss = 0.0f;
+    for (int c0 = sl * 8; c0 < cols; c0 += stride_cols) {
+        if (!row_ok) break;
+        float t[8];
+        load8<XD>(xr + c0, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(t[j], t[j], ss);
+    }
     for (int off = lpr >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-
     const float ms = ss / static_cast<float>(cols) + eps;
     const float r = 1.0f / __builtin_sqrtf(ms);
     if (!row_ok) return;
     YT* yr = y + row * ys;
-
-    auto emit = [&](int c0, const float (&t)[8]) {
-        float o[8];
-        if (HAS_W) {
-            float wf[8];
-            load8<WD>(w + c0, wf);
+    for (int c0 = sl * 8; c0 < cols; c0 += stride_cols) {
+        float t[8], o[8], wf[8];
+        load8<XD>(xr + c0, t);
+        if (HAS_W) load8<WD>(w + c0, wf);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = (t[j] * r) * wf[j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = t[j] * r;
+        for (int j = 0; j < 8; ++j) {
+            o[j] = t[j] * r;
+            if (HAS_W) o[j] = o[j] * wf[j];
+            o[j] = bf16_bits_to_f32(f32_to_bf16_bits(o[j]));
         }
-        // round to bf16 first (the reference stores bf16), then widen/narrow.
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = bf16_bits_to_f32(f32_to_bf16_bits(o[j]));
         store8<YD>(yr + c0, o);
-    };
-    if (NSTEP > 0) {
-#pragma unroll
-        for (int s = 0; s < NSTEP; ++s) {
-            const int c0 = s * stride_cols + sl * 8;
-            if (c0 < cols) emit(c0, v[s]);
-        }
-    } else {
-        for (int c0 = sl * 8; c0 < cols; c0 += stride_cols) {
-            float t[8];
-            load8<XD>(xr + c0, t);
-            emit(c0, t);
-        }
     }
 }
 

@@ -4,10 +4,14 @@ In a DiffusionGemma MoE layer the experts consume
 pre_feedforward_layernorm_2(residual) (TF modeling_diffusion_gemma.py:731-733):
   x_n = fused_rmsnorm(x, norm_w, eps)                     (kernels/fused_rmsnorm.py:24)
   y   = fused_moe_w4_v2(x_n, exp, topk_ids, topk_w)       (kernels/fused_moe_w4_v2.py:320)
-Five launches on the current stream (norm, route+prep, gate/up, down,
-combine), no host sync.
 
-LayerRunner issues the same five launches one C call at a time, with a
+moe_layer runs both as one C call, four launches on the current stream, no
+host sync: (1) routing + RMSNorm + fp16 activations, (2) gate/up + activation,
+(3) down, (4) fixed-order combine. The values are those of the two separate
+calls (the norm is rounded to bf16 before the fp16 conversion, as
+fused_rmsnorm's output is), which moe_layer_unfused runs for comparison.
+
+LayerRunner issues the same four launches one C call at a time, with a
 preallocated workspace, so a caller can record HIP events between them.
 """
 from __future__ import annotations
@@ -15,15 +19,55 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fused_moe_w4_v2 import _check_act, _check_weights, fused_moe_w4_v2
+from .fused_moe_w4_v2 import _check_act, _check_weights, fused_moe_w4_v2, moe_workspace
 from .fused_rmsnorm import fused_rmsnorm
 
-STAGES = ("rmsnorm", "route", "gateup", "down", "combine")
+STAGES = ("route_norm", "gateup", "down", "combine")
+
+
+def _prepare(exp, x, E, H, I):
+    if not getattr(exp, "_act_checked", False) or not hasattr(exp, "_ksl_act"):
+        _check_act(exp)
+    _check_weights(exp, E, H, I)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("moe_layer takes bf16 or fp16 activations")
+    if x.stride(1) != 1 or x.stride(0) % 8 != 0 or x.data_ptr() % 16 != 0:
+        x = x.contiguous()
+    return x
 
 
 @torch.no_grad()
 def moe_layer(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float, exp, topk_ids: torch.Tensor,
               topk_w: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    T, H = x.shape
+    tk = topk_ids.shape[1]
+    E, twoI, _ = exp.gu_q.shape
+    I = twoI // 2
+    x = _prepare(exp, x, E, H, I)
+    ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)
+    ids = ids.contiguous()
+    w = topk_w.contiguous()
+    nw = None if norm_w is None else norm_w.reshape(-1).contiguous()
+    y = torch.empty(T, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return y
+    if workspace is None:
+        workspace = moe_workspace(T, tk, E, H, I, x.device)
+    rc = _lib.load().ksl_moe_layer_forward(
+        _lib.ptr(x), _lib.dtype_code(x.dtype), x.stride(0), _lib.ptr(nw),
+        _lib.dtype_code(nw.dtype) if nw is not None else _lib.DTYPE_BF16, float(eps),
+        _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
+        _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z),
+        T, tk, E, H, I, exp._ksl_act, _lib.ptr(y), _lib.dtype_code(y.dtype), y.stride(0),
+        _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x))
+    _lib.check(rc, "ksl_moe_layer_forward")
+    return y
+
+
+@torch.no_grad()
+def moe_layer_unfused(x, norm_w, eps, exp, topk_ids, topk_w, workspace=None):
+    """The same layer as two drop-in calls (norm, then the MoE forward)."""
     xn = fused_rmsnorm(x, norm_w, eps)
     return fused_moe_w4_v2(xn, exp, topk_ids, topk_w, workspace=workspace)
 
@@ -35,7 +79,6 @@ class LayerRunner:
         self.T, self.topk, self.E, self.H, self.I = T, topk, E, H, I
         self.device = torch.device(device)
         nexp = T * topk
-        self.xn = torch.empty(T, H, dtype=act_dtype, device=device)
         self.sorted_rows = torch.empty(nexp, dtype=torch.int32, device=device)
         self.offsets = torch.empty(E + 1, dtype=torch.int32, device=device)
         self.inv = torch.empty(nexp, dtype=torch.int32, device=device)
@@ -47,41 +90,36 @@ class LayerRunner:
 
     @torch.no_grad()
     def run(self, x, norm_w, eps, exp, topk_ids, topk_w, events=None):
-        """events: optional list of 6 torch.cuda.Event recorded before, between
-        and after the five launches."""
+        """events: optional list of len(STAGES)+1 torch.cuda.Event recorded
+        before, between and after the launches."""
         L, p = self.lib, _lib.ptr
         T, tk, E, H, I = self.T, self.topk, self.E, self.H, self.I
-        if not getattr(exp, "_act_checked", False) or not hasattr(exp, "_ksl_act"):
-            _check_act(exp)
-        _check_weights(exp, E, H, I)
+        x = _prepare(exp, x, E, H, I)
         st = _lib.stream_of(x)
         code = _lib.dtype_code(x.dtype)
         ev = events
         if ev:
             ev[0].record()
-        rc = L.ksl_rmsnorm(p(x), code, p(norm_w), _lib.dtype_code(norm_w.dtype) if norm_w is not None else code,
-                           p(self.xn), code, T, H, x.stride(0), H, float(eps), st)
-        _lib.check(rc, "ksl_rmsnorm")
+        rc = L.ksl_moe_layer_route(p(topk_ids), T, tk, E, p(self.sorted_rows), p(self.offsets), p(self.inv),
+                                   p(x), code, x.stride(0), p(norm_w),
+                                   _lib.dtype_code(norm_w.dtype) if norm_w is not None else code, float(eps),
+                                   H, p(self.a16), st)
+        _lib.check(rc, "ksl_moe_layer_route")
         if ev:
             ev[1].record()
-        rc = L.ksl_moe_route(p(topk_ids), T, tk, E, p(self.sorted_rows), p(self.offsets), p(self.inv),
-                             p(self.xn), code, H, H, p(self.a16), st)
-        _lib.check(rc, "ksl_moe_route")
-        if ev:
-            ev[2].record()
         rc = L.ksl_moe_gateup_act(p(self.a16), p(self.sorted_rows), p(self.offsets), tk, p(exp.gu_q),
                                   p(exp.gu_s), p(exp.gu_z), E, H, I, exp._ksl_act, p(self.out2), st)
         _lib.check(rc, "ksl_moe_gateup_act")
         if ev:
-            ev[3].record()
+            ev[2].record()
         rc = L.ksl_moe_down(p(self.out2), p(self.offsets), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z), E, H, I,
                             p(self.out3), st)
         _lib.check(rc, "ksl_moe_down")
         if ev:
-            ev[4].record()
+            ev[3].record()
         rc = L.ksl_moe_combine(p(self.out3), p(self.inv), p(topk_w), _lib.dtype_code(topk_w.dtype), T, tk, H,
                                p(self.y), code, H, st)
         _lib.check(rc, "ksl_moe_combine")
         if ev:
-            ev[5].record()
+            ev[4].record()
         return self.y

@@ -43,14 +43,15 @@ MOE_MAX_TOL = 2e-2
 MOE_MEAN_TOL = 1e-2
 
 
-def unperm8(a: np.ndarray) -> np.ndarray:
-    """Undo the K-slot storage order {0,4,1,5,2,6,3,7} of 8-element blocks."""
+def act_unperm(a: np.ndarray, gs: int) -> np.ndarray:
+    """Undo the expert-GEMM activation storage order along the last axis: within
+    each group of gs elements, logical offset o = c*(gs/4) + i*8 + j is stored
+    at i*32 + c*8 + s(j), with s the inverse of the K-slot order {0,4,1,5,2,6,3,7}."""
     n = a.shape[-1]
-    perm = np.array([0, 4, 1, 5, 2, 6, 3, 7])
-    idx = (np.arange(n) // 8) * 8
-    src = np.empty(n, dtype=np.int64)
-    # storage index s holds logical (s//8)*8 + perm[s%8]
-    s = np.arange(n)
-    src[(s // 8) * 8 + perm[s % 8]] = s
-    del idx
-    return a[..., src]
+    q = gs // 4
+    o = np.arange(n) % gs
+    g0 = np.arange(n) - o
+    c, i, j = o // q, (o % q) // 8, o % 8
+    sj = np.where(j < 4, 2 * j, 2 * (j - 4) + 1)
+    store = g0 + i * 32 + c * 8 + sj
+    return a[..., store]
