@@ -64,24 +64,23 @@ __device__ __forceinline__ float act_times_up(float g, float u) {
 }
 
 // ---------------------------------------------------------------- gate / up
-// Producer / consumer workgroup: 4 consumer waves (each one gate tile and one
-// up tile of 16 columns of I) and 4 producer waves. Producers only issue
-// global loads - the workgroup's weights and gathered activations for one
-// quantisation group (128 K) at a time - keep kGuLead groups in flight in
-// their registers, and write each arrived group into a two-slot LDS ring.
-// Consumers only read LDS, decode and run MFMA; they never wait on memory
-// counters. One barrier per group hands a slot from producers to consumers.
-constexpr int kGuCons = 4;                       // consumer waves
-constexpr int kGuProd = 4;                       // producer waves
-constexpr int kGuWgCols = 16 * kGuCons;          // 64 columns of I per workgroup
-constexpr int kGuThreads = (kGuCons + kGuProd) * kWave;  // 512
-constexpr int kGuLead = 4;                       // groups of loads in flight per producer
+// One workgroup covers NC*16 columns of I of one expert (NC = 11: 176 columns,
+// a quarter of DiffusionGemma's I = 704) with NC consumer waves and NP
+// producer waves:
+//   - consumer w owns columns w*16 .. w*16+15: one gate tile and one up tile
+//     of 16 weight rows; it only reads LDS, decodes nibbles and runs MFMA;
+//   - producers only issue global loads: per quantisation group (128 K) all
+//     2*NC weight fragment blocks (16 rows x 64 B) and the 4*MT activation
+//     fragment blocks, two groups in flight, and write them into a ring of two
+//     half-group slots (64 K each) in LDS.
+// One barrier per half group hands a slot from producers to consumers. Wide
+// workgroups keep the activation re-reads small (every requested byte costs
+// load bandwidth, L2 hit or not): the gathered rows of an expert are read
+// I/(16*NC) times per layer instead of once per 64-column block.
 constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
-constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
-constexpr int kGuSlotW = 2 * kGuCons * kBlk;     // 8 KB of weights per group
-constexpr int kGuSlot = kGuSlotW + kMaxMt * 4 * kBlk;  // + 8 KB of activations
+constexpr int kBlk = kWave * 16;                 // one full-group fragment block: 64 lanes x 16 B
+constexpr int kHalfBlk = kWave * 8;              // one half-group weight block: 64 lanes x 8 B
 constexpr int kGuMaxG = 32;                      // H <= 4096
-constexpr int kGuSzPer = 4 * 32 * kGuMaxG / (kGuProd * kWave);  // scale/zero dwords per producer lane
 
 struct GuArgs {
     const f16* a16;
@@ -94,184 +93,254 @@ struct GuArgs {
     int topk, I, H;
 };
 
-// Producer wave p (0..3) loads, per group: the gate and up fragment blocks of
-// consumer wave p (lane L = c*16 + col: row col of the tile, bytes c*16.. of
-// the group's 64) and the activation blocks (t, i = p) for t < MT (lane L:
-// row t*16 + L%16, stored chunk g*128 + p*32 + (L/16)*8: 64 contiguous bytes
-// per row, see act_store_index).
-template <int MT>
-struct GuProducer {
-    const uint8_t* wq0;   // gate row, + c*16
-    const uint8_t* wq1;   // up row
-    const f16* ar[MT];    // activation row (gathered token), + c*32 + p*8
-    u32x4 v[kGuLead][2 + MT];
-
-    __device__ __forceinline__ void load(int g, u32x4 (&dst)[2 + MT]) const {
-        dst[0] = *reinterpret_cast<const u32x4*>(wq0 + g * 64);
-        dst[1] = *reinterpret_cast<const u32x4*>(wq1 + g * 64);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) dst[2 + t] = *reinterpret_cast<const u32x4*>(ar[t] + g * 128);
-    }
-    __device__ __forceinline__ void store(char* slot, int p, int lane, const u32x4 (&src)[2 + MT]) const {
-        *reinterpret_cast<u32x4*>(slot + (p * 2 + 0) * kBlk + lane * 16) = src[0];
-        *reinterpret_cast<u32x4*>(slot + (p * 2 + 1) * kBlk + lane * 16) = src[1];
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-            *reinterpret_cast<u32x4*>(slot + kGuSlotW + (t * 4 + p) * kBlk + lane * 16) = src[2 + t];
-    }
+template <int NC, int NP>
+struct GuShape {
+    static constexpr int kCols = 16 * NC;                      // columns of I per workgroup
+    static constexpr int kThreads = (NC + NP) * kWave;
+    static constexpr int kSlotW = 2 * NC * kHalfBlk;           // weight bytes per half slot
+    static constexpr int kSlot = kSlotW + kMaxMt * 2 * kBlk;   // + activation bytes per half slot
+    static constexpr int kSzBytesMaxG = 4 * kCols * kGuMaxG * 2;
+    static constexpr int kSzPer = (kSzBytesMaxG / 16 + kThreads - 1) / kThreads;  // 16-B scale chunks per thread
+    static size_t lds_bytes(int G) { return 2 * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
 };
 
-template <int ACT, int MT>
-__device__ __forceinline__ void gateup_chunk(const GuArgs& A, int e, int nb, char* __restrict__ lds,
-                                             const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
+// Producer side of one row chunk: 1 + 2*Gp barriers (Gp = G rounded up to even).
+template <int NC, int NP, int MT>
+__device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
+                                               int m0, int mrows) {
+    using S = GuShape<NC, NP>;
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
     const int G = A.H >> 7;
-    const int Gp = (G + kGuLead - 1) / kGuLead * kGuLead;  // groups padded to whole load rounds
-    char* slot0 = lds;
-
-    if (wave >= kGuCons) {
-        // ------------------------------------------------------------ producer
-        const int p = wave - kGuCons;
-        GuProducer<MT> P;
-        const int64_t rg = static_cast<int64_t>(e) * 2 * A.I + nb * kGuWgCols + p * 16 + col;
-        P.wq0 = A.gu_q + rg * (A.H >> 1) + c * 16;
-        P.wq1 = A.gu_q + (rg + A.I) * (A.H >> 1) + c * 16;
+    {
+        // blocks b = p + NP*k: b < 2*NC -> weight block (w = b/2, tile j = b%2:
+        // gate, up), else activation block (t, i) = ((b - 2*NC)/4, (b - 2*NC)%4).
+        // Past the last block: clamped (a duplicate load and an identical LDS write).
+        constexpr int NB = 2 * NC + 4 * MT;
+        constexpr int KP = (NB + NP - 1) / NP;
+        const int p = wave - NC;
+        uint32_t off[KP];    // offset of group 0 from gu_q / a16, in 16-byte units (all terms are)
+        int dst[KP];         // LDS byte offset of the block within a half slot (lane included)
+        bool isw[KP];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            int r = t * 16 + col;
-            if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
-            const int tok = A.sorted_rows[start + m0 + r] / A.topk;
-            P.ar[t] = A.a16 + static_cast<int64_t>(tok) * A.H + p * 32 + c * 8;
-        }
-        // prologue: groups 0..kGuLead-1 in flight, group 0 into slot 0
-#pragma unroll
-        for (int u = 0; u < kGuLead; ++u) P.load(u < G ? u : G - 1, P.v[u]);
-        P.store(slot0, p, lane, P.v[0]);
-        __syncthreads();
-        // step i: group i+1 (set (i+1)%L) -> slot (i+1)%2; loads of group i+L -> set i%L
-        for (int g0 = 0; g0 < Gp; g0 += kGuLead) {
-#pragma unroll
-            for (int u = 0; u < kGuLead; ++u) {
-                const int i = g0 + u;
-                P.store(slot0 + ((i + 1) & 1) * kGuSlot, p, lane, P.v[(u + 1) % kGuLead]);
-                const int gl = i + kGuLead < G ? i + kGuLead : G - 1;
-                P.load(gl, P.v[u]);
-                __syncthreads();
+        for (int k = 0; k < KP; ++k) {
+            int b = p + NP * k;
+            if (b >= NB) b = NB - 1;
+            isw[k] = b < 2 * NC;
+            if (isw[k]) {
+                const int w = b >> 1, j = b & 1;
+                const int64_t row = static_cast<int64_t>(e) * 2 * A.I + (j ? A.I : 0) + c0 + w * 16 + col;
+                off[k] = static_cast<uint32_t>((row * (A.H >> 1) + c * 16) >> 4);
+                dst[k] = (b * kWave + lane) * 8;
+            } else {
+                const int a = b - 2 * NC, t = a >> 2, i = a & 3;
+                int r = t * 16 + col;
+                if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
+                const int tok = A.sorted_rows[start + m0 + r] / A.topk;
+                off[k] = static_cast<uint32_t>((static_cast<int64_t>(tok) * A.H + i * 32 + c * 8) >> 3);
+                dst[k] = S::kSlotW + ((t * 2 + (i & 1)) * kWave + lane) * 16 + (i >> 1) * (1 << 30);
             }
         }
-        return;
+        const char* wbase = reinterpret_cast<const char*>(A.gu_q);
+        const char* abase = reinterpret_cast<const char*>(A.a16);
+        u32x4 v[2][KP];
+        auto load_group = [&](int g, u32x4 (&dstv)[KP]) {
+            const int gc = g < G ? g : G - 1;
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const char* src = isw[k] ? wbase + static_cast<uint64_t>(off[k]) * 16 + gc * 64
+                                         : abase + static_cast<uint64_t>(off[k]) * 16 + gc * 256;
+                dstv[k] = *reinterpret_cast<const u32x4*>(src);
+            }
+        };
+        // half hh of a group into slot `slot`: weight blocks give 8 bytes per half,
+        // activation blocks belong to half i/2 (encoded in bit 30 of dst)
+        auto store_half = [&](int hh, const u32x4 (&srcv)[KP]) {
+            char* base = lds + hh * S::kSlot;
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                if (isw[k]) {
+                    const u32x2 h = hh ? u32x2{srcv[k][2], srcv[k][3]} : u32x2{srcv[k][0], srcv[k][1]};
+                    *reinterpret_cast<u32x2*>(base + dst[k]) = h;
+                } else if ((dst[k] >> 30) == hh) {
+                    *reinterpret_cast<u32x4*>(base + (dst[k] & ((1 << 30) - 1))) = srcv[k];
+                }
+            }
+        };
+        load_group(0, v[0]);
+        load_group(1, v[1]);
+        store_half(0, v[0]);
+        __syncthreads();
+        // half step s: consumers read slot s%2; producers fill slot (s+1)%2 with
+        // half step s+1: (s even) half 1 of group s/2, (s odd) half 0 of group s/2+1.
+        for (int g = 0; g < G; g += 2) {
+            // s = 2g
+            store_half(1, v[0]);
+            load_group(g + 2, v[0]);
+            __syncthreads();
+            // s = 2g + 1
+            store_half(0, v[1]);
+            __syncthreads();
+            // s = 2g + 2
+            store_half(1, v[1]);
+            load_group(g + 3, v[1]);
+            __syncthreads();
+            // s = 2g + 3
+            store_half(0, v[0]);
+            __syncthreads();
+        }
     }
+}
 
-    // -------------------------------------------------------------- consumer
+// Consumer side of one row chunk: 1 + 2*Gp barriers, matching gateup_produce.
+template <int ACT, int NC, int NP, int MT>
+__device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
+                                               const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
+    using S = GuShape<NC, NP>;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int col = lane & 15, c = lane >> 4;
+    const int G = A.H >> 7;
     const NibConsts kn = nib_consts();
-    const f16* sg = lds_sz;
-    const f16* zg = lds_sz + 64 * G;
-    const f16* su = lds_sz + 2 * 64 * G;
-    const f16* zu = lds_sz + 3 * 64 * G;
-    const int wcol = wave * 16 + col;  // row of this lane within the workgroup's 64
-    f32x4 acc[2][MT];
+    const int kc = S::kCols;
+    const f16* s_g = lds_sz;
+    const f16* z_g = lds_sz + kc * G;
+    const f16* s_u = lds_sz + 2 * kc * G;
+    const f16* z_u = lds_sz + 3 * kc * G;
+    f32x4 acc[2][MT], part[2][MT];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();  // slot 0 and the scale table are ready
-    for (int i = 0; i < Gp; ++i) {
-        if (i < G) {
-            const char* slot = slot0 + (i & 1) * kGuSlot;
-            const u32x4 w0 = *reinterpret_cast<const u32x4*>(slot + (wave * 2 + 0) * kBlk + lane * 16);
-            const u32x4 w1 = *reinterpret_cast<const u32x4*>(slot + (wave * 2 + 1) * kBlk + lane * 16);
-            const float s0 = static_cast<float>(sg[wcol * G + i]);
-            const float s1 = static_cast<float>(su[wcol * G + i]);
-            const ZeroPair zc0 = zero_pair(zg[wcol * G + i]);
-            const ZeroPair zc1 = zero_pair(zu[wcol * G + i]);
-            f32x4 part[2][MT];
+    const int Gp = (G + 1) & ~1;  // producers run whole pairs of groups
+    for (int s = 0; s < 2 * Gp; ++s) {
+        const int g = s >> 1, hh = s & 1;
+        if (g < G) {
+            const char* slot = lds + hh * S::kSlot;
+            if (hh == 0) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            const int r = wave * 16 + col;  // row of the tile within the workgroup
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const f16x8 b0 = nib8_minus_zero(w0[k], zc0, kn);
-                const f16x8 b1 = nib8_minus_zero(w1[k], zc1, kn);
+            for (int j = 0; j < 2; ++j) {
+                const ZeroPair zc = zero_pair((j ? z_u : z_g)[r * G + g]);
+                const u32x2 wv = *reinterpret_cast<const u32x2*>(slot + ((wave * 2 + j) * kWave + lane) * 8);
 #pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const f16x8 a = *reinterpret_cast<const f16x8*>(slot + kGuSlotW + (t * 4 + k) * kBlk + lane * 16);
-                    part[0][t] = mfma16x16x32(a, b0, part[0][t]);
-                    part[1][t] = mfma16x16x32(a, b1, part[1][t]);
+                for (int ii = 0; ii < 2; ++ii) {
+                    const f16x8 b = nib8_minus_zero(wv[ii], zc, kn);
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const f16x8 a = *reinterpret_cast<const f16x8*>(slot + S::kSlotW + ((t * 2 + ii) * kWave + lane) * 16);
+                        part[j][t] = mfma16x16x32(a, b, part[j][t]);
+                    }
                 }
             }
+            if (hh == 1) {
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
+                for (int j = 0; j < 2; ++j) {
+                    const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc[0][t][r] = __builtin_fmaf(s0, part[0][t][r], acc[0][t][r]);
-                    acc[1][t][r] = __builtin_fmaf(s1, part[1][t][r], acc[1][t][r]);
+                    for (int t = 0; t < MT; ++t)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
                 }
+            }
         }
         __syncthreads();
     }
-    const int n0 = nb * kGuWgCols + wave * 16;
-    const int sc = act_store_index<64>(n0 + col);  // out2 is the down GEMM's activation
-    f16* o = A.out2 + static_cast<int64_t>(start + m0) * A.I + sc;
+    // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
+    {
+        const int sc = act_store_index<64>(c0 + wave * 16 + col);  // out2 is the down GEMM's activation
+        f16* o = A.out2 + static_cast<int64_t>(start + m0) * A.I + sc;
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+        for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = t * 16 + 4 * c + r;
-            if (row < mrows)
-                o[static_cast<int64_t>(row) * A.I] = static_cast<f16>(act_times_up<ACT>(acc[0][t][r], acc[1][t][r]));
-        }
+            for (int q = 0; q < 4; ++q) {
+                const int row = t * 16 + 4 * c + q;
+                if (row < mrows)
+                    o[static_cast<int64_t>(row) * A.I] = static_cast<f16>(act_times_up<ACT>(acc[0][t][q], acc[1][t][q]));
+            }
+    }
 }
 
-template <int ACT>
-__global__ __launch_bounds__(kGuThreads) __attribute__((amdgpu_waves_per_eu(4))) void gateup_act_kernel(GuArgs A) {
+template <int ACT, int NC, int NP>
+__global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A) {
+    using S = GuShape<NC, NP>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const int nb_per_e = A.I / kGuWgCols;
+    const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
     const int e = tile / nb_per_e;
-    const int nb = tile - e * nb_per_e;
+    const int c0 = (tile - e * nb_per_e) * S::kCols;
     const int start = A.offsets[e];
     const int M = A.offsets[e + 1] - start;
     if (M <= 0) return;
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    f16* lds_sz = reinterpret_cast<f16*>(lds + 2 * kGuSlot);
-    // scales / zeros of the 64 gate and 64 up rows: four [64 x G] fp16 blocks
-    // (s_gate, z_gate, s_up, z_up), copied by the producers; published by the
-    // first barrier of the first chunk.
-    if (wave >= kGuCons) {
-        const int pt = tid - kGuCons * kWave;
-        const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + nb * kGuWgCols;
+    f16* lds_sz = reinterpret_cast<f16*>(lds + 2 * S::kSlot);
+    // scale / zero table of the workgroup's rows: four [kCols x G] fp16 blocks
+    // (s_gate, z_gate, s_up, z_up), each contiguous in global memory and
+    // 16-byte aligned; copied by all waves, published by the first barrier.
+    {
+        const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + c0;
         const int64_t up0 = gate0 + A.I;
-        const int nd = 32 * G;  // dwords per block (block starts are 4-byte aligned)
-        uint32_t v[kGuSzPer];
+        const int nq = S::kCols * G * 2 / 16;  // 16-byte chunks per block
+        u32x4 v[S::kSzPer];
 #pragma unroll
-        for (int k = 0; k < kGuSzPer; ++k) {
-            int i = pt + k * kGuProd * kWave;
-            if (i >= 4 * nd) i = 0;  // clamped, never stored
-            const int b = i / nd, o = i - b * nd;
+        for (int k = 0; k < S::kSzPer; ++k) {
+            int i = tid + k * S::kThreads;
+            if (i >= 4 * nq) i = 0;  // clamped, never stored
+            const int b = i / nq, o = i - b * nq;
             const f16* base = ((b & 1) ? A.gu_z : A.gu_s) + ((b & 2) ? up0 : gate0) * G;
-            v[k] = reinterpret_cast<const uint32_t*>(base)[o];
+            v[k] = reinterpret_cast<const u32x4*>(base)[o];
         }
-        uint32_t* d = reinterpret_cast<uint32_t*>(lds_sz);
 #pragma unroll
-        for (int k = 0; k < kGuSzPer; ++k) {
-            const int i = pt + k * kGuProd * kWave;
-            if (i < 4 * nd) d[i] = v[k];
+        for (int k = 0; k < S::kSzPer; ++k) {
+            const int i = tid + k * S::kThreads;
+            if (i < 4 * nq) reinterpret_cast<u32x4*>(lds_sz)[i] = v[k];
         }
     }
-    for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
-        const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
-        if (mrows <= 16)
-            gateup_chunk<ACT, 1>(A, e, nb, lds, lds_sz, start, m0, mrows);
-        else
-            gateup_chunk<ACT, 2>(A, e, nb, lds, lds_sz, start, m0, mrows);
-        __syncthreads();  // ring free for the next chunk
+    // Roles split once; both loops run the same chunks with the same barrier count.
+    if (tid / kWave >= NC) {
+        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
+            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+            if (mrows <= 16)
+                gateup_produce<NC, NP, 1>(A, e, c0, lds, start, m0, mrows);
+            else
+                gateup_produce<NC, NP, 2>(A, e, c0, lds, start, m0, mrows);
+            __syncthreads();  // ring free for the next chunk
+        }
+    } else {
+        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
+            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+            if (mrows <= 16)
+                gateup_consume<ACT, NC, NP, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+            else
+                gateup_consume<ACT, NC, NP, 2>(A, c0, lds, lds_sz, start, m0, mrows);
+            __syncthreads();  // ring free for the next chunk
+        }
     }
+}
+
+template <int NC, int NP>
+int launch_gateup_nc(const GuArgs& A, int64_t E, int act, hipStream_t st) {
+    using S = GuShape<NC, NP>;
+    const unsigned grid = static_cast<unsigned>(E * (A.I / S::kCols));
+    const size_t lds = S::lds_bytes(A.H / 128);
+    if (act == KSL_ACT_GELU_TANH)
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP>), dim3(grid), dim3(S::kThreads), lds, st, A);
+    else if (act == KSL_ACT_SILU)
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP>), dim3(grid), dim3(S::kThreads), lds, st, A);
+    else
+        return KSL_ERR_ARG;
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }
 
 // --------------------------------------------------------------------- down
@@ -471,10 +540,10 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
                   int64_t I, int act, void* out2, hipStream_t st) {
     if (!a16 || !sorted_rows || !offsets || !gu_q || !gu_s || !gu_z || !out2) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0 || topk <= 0) return KSL_ERR_SHAPE;
-    if (H % 128 != 0 || I % kGuWgCols != 0 || H > 128 * kGuMaxG) return KSL_ERR_SHAPE;
-    if (E * 2 * I * (H / 2) >= (int64_t(1) << 40)) return KSL_ERR_SHAPE;
+    if (H % 128 != 0 || I % 64 != 0 || H > 128 * kGuMaxG) return KSL_ERR_SHAPE;
+    if (E * 2 * I * (H / 2) >= (int64_t(1) << 36)) return KSL_ERR_SHAPE;  // 32-bit offsets in 16-B units
     if (reinterpret_cast<uintptr_t>(gu_q) % 16 || reinterpret_cast<uintptr_t>(a16) % 16 ||
-        reinterpret_cast<uintptr_t>(gu_s) % 4 || reinterpret_cast<uintptr_t>(gu_z) % 4 ||
+        reinterpret_cast<uintptr_t>(gu_s) % 16 || reinterpret_cast<uintptr_t>(gu_z) % 16 ||
         reinterpret_cast<uintptr_t>(out2) % 2)
         return KSL_ERR_ALIGN;
     GuArgs A;
@@ -488,16 +557,10 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     A.topk = static_cast<int>(topk);
     A.I = static_cast<int>(I);
     A.H = static_cast<int>(H);
-    const unsigned grid = static_cast<unsigned>(E * (I / kGuWgCols));
-    const size_t lds = 2 * kGuSlot + 4 * 64 * (H / 128) * sizeof(f16);
-    if (act == KSL_ACT_GELU_TANH)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH>), dim3(grid), dim3(kGuThreads), lds, st, A);
-    else if (act == KSL_ACT_SILU)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU>), dim3(grid), dim3(kGuThreads), lds, st, A);
-    else
-        return KSL_ERR_ARG;
-    KSL_LAUNCH_CHECK();
-    return KSL_OK;
+    // widest column block that divides I: 176 (11 consumers), 128, or 64
+    if (I % 176 == 0) return launch_gateup_nc<11, 5>(A, E, act, st);
+    if (I % 128 == 0) return launch_gateup_nc<8, 4>(A, E, act, st);
+    return launch_gateup_nc<4, 4>(A, E, act, st);
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,

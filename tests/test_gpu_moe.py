@@ -131,6 +131,8 @@ STAGE_CASES = [
     (16, 2, 4, 256, 128, 31),
     (64, 8, 16, 512, 192, 32),
     (256, 8, 128, 2816, 704, 33),
+    (48, 4, 8, 384, 704, 34),    # odd number of 128-groups, 176-column blocks
+    (40, 4, 4, 640, 128, 35),    # odd number of 128-groups, 128-column blocks
 ]
 
 
