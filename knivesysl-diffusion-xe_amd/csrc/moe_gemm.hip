@@ -69,17 +69,69 @@ __device__ __forceinline__ float act_times_up(float g, float u) {
 // producer waves:
 //   - consumer w owns columns w*16 .. w*16+15: one gate tile and one up tile
 //     of 16 weight rows; it only reads LDS, decodes nibbles and runs MFMA;
-//   - producers only issue global loads: per quantisation group (128 K) all
-//     2*NC weight fragment blocks (16 rows x 64 B) and the 4*MT activation
-//     fragment blocks, two groups in flight, and write them into a ring of two
-//     half-group slots (64 K each) in LDS.
-// One barrier per half group hands a slot from producers to consumers. Wide
+//   - producers only issue direct global->LDS loads: per quantisation group
+//     (128 K) all 2*NC weight fragment blocks (16 rows x 64 B) and the 4*MT
+//     activation fragment blocks go into one slot of an R-slot LDS ring, with
+//     up to R-1 groups in flight and no register staging; each block is
+//     fetched row-major and lands in the swizzled order of frag_pos.
+// One barrier per group hands a slot from producers to consumers. Wide
 // workgroups keep the activation re-reads small (every requested byte costs
 // load bandwidth, L2 hit or not): the gathered rows of an expert are read
 // I/(16*NC) times per layer instead of once per 64-column block.
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* gbl_vptr;
+
+// Direct global -> LDS copy of one fragment block: lane L's 16 bytes land at
+// lds_block + 16*L. lds_block must be wave-uniform. Completion is tracked by
+// the issuing wave's vmcnt only.
+__device__ __forceinline__ void dma16(const void* src, char* lds_block) {
+    __builtin_amdgcn_global_load_lds((gbl_vptr)(const_cast<void*>(src)), (lds_vptr)lds_block, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N), other counters left free (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most n groups of k loads each are outstanding, n in [0, NMAX].
+template <int K, int NMAX>
+__device__ __forceinline__ void vm_wait_groups(int n) {
+    if constexpr (NMAX > 0) {
+        if (n >= NMAX) {
+            vm_wait<NMAX * K>();
+            return;
+        }
+        vm_wait_groups<K, NMAX - 1>(n);
+    } else {
+        vm_wait<0>();
+    }
+}
+
+// Workgroup barrier of a wave whose only LDS writes are direct global->LDS
+// loads that it has already waited for with vm_wait. __syncthreads() would
+// add s_waitcnt vmcnt(0) for the still-pending loads of later groups and
+// drain the ring; the asm statements keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void dma_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
-constexpr int kBlk = kWave * 16;                 // one full-group fragment block: 64 lanes x 16 B
-constexpr int kHalfBlk = kWave * 8;              // one half-group weight block: 64 lanes x 8 B
+
+// LDS position (16-byte unit) of MFMA lane (row, k-group c) within a fragment
+// block of 16 rows x 64 bytes. Blocks are fetched row-major (4 consecutive
+// lanes per 64-byte row: whole 64-byte segments per 4 lanes, which streams
+// faster than 16 rows per 4 lanes), and chunk c of row r sits at
+// r*4 + (c ^ (r/4 % 4)) so that the 16 lanes of one k-group read 16 distinct
+// 16-byte bank groups.
+__device__ __forceinline__ int frag_pos(int row, int c) { return row * 4 + (c ^ ((row >> 2) & 3)); }
+constexpr size_t kLdsBytes = 160 * 1024;         // LDS per workgroup on gfx950
+constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
 constexpr int kGuMaxG = 32;                      // H <= 4096
 
 struct GuArgs {
@@ -93,115 +145,93 @@ struct GuArgs {
     int topk, I, H;
 };
 
-template <int NC, int NP>
+template <int NC, int NP, int R>
 struct GuShape {
     static constexpr int kCols = 16 * NC;                      // columns of I per workgroup
     static constexpr int kThreads = (NC + NP) * kWave;
-    static constexpr int kSlotW = 2 * NC * kHalfBlk;           // weight bytes per half slot
-    static constexpr int kSlot = kSlotW + kMaxMt * 2 * kBlk;   // + activation bytes per half slot
-    static constexpr int kSzBytesMaxG = 4 * kCols * kGuMaxG * 2;
-    static constexpr int kSzPer = (kSzBytesMaxG / 16 + kThreads - 1) / kThreads;  // 16-B scale chunks per thread
-    static size_t lds_bytes(int G) { return 2 * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
+    static constexpr int kSlotW = 2 * NC * kBlk;               // weight bytes per slot
+    static constexpr int kSlot = kSlotW + 4 * kMaxMt * kBlk;   // + activation bytes per slot
+    static constexpr int kSzPer = (4 * kCols * kGuMaxG * 2 / 16 + NC * kWave - 1) / (NC * kWave);
+    static size_t lds_bytes(int G) { return static_cast<size_t>(R) * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
 };
 
-// Producer side of one row chunk: 1 + 2*Gp barriers (Gp = G rounded up to even).
-template <int NC, int NP, int MT>
+// Producer side of one row chunk: 1 + G barriers. Slot of group g: g % R.
+// Wave p issues blocks b = p + NP*k (k < KP, b < NB): b < 2*NC is weight block
+// (w, j) = (b/2, b%2) (j: gate, up), else activation block (t, i) =
+// ((b - 2*NC)/4, (b - 2*NC)%4) of M tile t and 32-K step i.
+template <int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
                                                int m0, int mrows) {
-    using S = GuShape<NC, NP>;
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid & (kWave - 1);
-    const int col = lane & 15, c = lane >> 4;
+    using S = GuShape<NC, NP, R>;
+    constexpr int NB = 2 * NC + 4 * MT;
+    constexpr int KP = (NB + NP - 1) / NP;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int p = threadIdx.x / kWave - NC;
+    // row-major fetch: lanes 4r .. 4r+3 cover the 64 bytes of block row r
+    // (4 rows per 256 B), chunk order swizzled per row (frag_pos)
+    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
     const int G = A.H >> 7;
-    {
-        // blocks b = p + NP*k: b < 2*NC -> weight block (w = b/2, tile j = b%2:
-        // gate, up), else activation block (t, i) = ((b - 2*NC)/4, (b - 2*NC)%4).
-        // Past the last block: clamped (a duplicate load and an identical LDS write).
-        constexpr int NB = 2 * NC + 4 * MT;
-        constexpr int KP = (NB + NP - 1) / NP;
-        const int p = wave - NC;
-        uint32_t off[KP];    // offset of group 0 from gu_q / a16, in 16-byte units (all terms are)
-        int dst[KP];         // LDS byte offset of the block within a half slot (lane included)
-        bool isw[KP];
+    const bool full = p + NP * (KP - 1) < NB;  // this wave issues KP blocks per group, else KP - 1
+    const char* src[KP];
+    int dst[KP];   // LDS byte offset of the block within a slot
+    int gstep[KP]; // global bytes per group
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            int b = p + NP * k;
-            if (b >= NB) b = NB - 1;
-            isw[k] = b < 2 * NC;
-            if (isw[k]) {
-                const int w = b >> 1, j = b & 1;
-                const int64_t row = static_cast<int64_t>(e) * 2 * A.I + (j ? A.I : 0) + c0 + w * 16 + col;
-                off[k] = static_cast<uint32_t>((row * (A.H >> 1) + c * 16) >> 4);
-                dst[k] = (b * kWave + lane) * 8;
-            } else {
-                const int a = b - 2 * NC, t = a >> 2, i = a & 3;
-                int r = t * 16 + col;
-                if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
-                const int tok = A.sorted_rows[start + m0 + r] / A.topk;
-                off[k] = static_cast<uint32_t>((static_cast<int64_t>(tok) * A.H + i * 32 + c * 8) >> 3);
-                dst[k] = S::kSlotW + ((t * 2 + (i & 1)) * kWave + lane) * 16 + (i >> 1) * (1 << 30);
-            }
+    for (int k = 0; k < KP; ++k) {
+        int b = p + NP * k;
+        if (b >= NB) b = NB - 1;  // never issued
+        if (b < 2 * NC) {
+            const int w = b >> 1, j = b & 1;
+            const int64_t row = static_cast<int64_t>(e) * 2 * A.I + (j ? A.I : 0) + c0 + w * 16 + rr;
+            src[k] = reinterpret_cast<const char*>(A.gu_q) + row * (A.H >> 1) + ch * 16;
+            gstep[k] = 64;
+        } else {
+            const int a = b - 2 * NC, t = a >> 2, i = a & 3;
+            int r = t * 16 + rr;
+            if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
+            const int tok = A.sorted_rows[start + m0 + r] / A.topk;
+            src[k] = reinterpret_cast<const char*>(A.a16 + static_cast<int64_t>(tok) * A.H + i * 32 + ch * 8);
+            gstep[k] = 256;
         }
-        const char* wbase = reinterpret_cast<const char*>(A.gu_q);
-        const char* abase = reinterpret_cast<const char*>(A.a16);
-        u32x4 v[2][KP];
-        auto load_group = [&](int g, u32x4 (&dstv)[KP]) {
-            const int gc = g < G ? g : G - 1;
+        dst[k] = b * kBlk;
+    }
+    auto issue = [&](int g, int slot) {
+        char* base = lds + slot * S::kSlot;
 #pragma unroll
-            for (int k = 0; k < KP; ++k) {
-                const char* src = isw[k] ? wbase + static_cast<uint64_t>(off[k]) * 16 + gc * 64
-                                         : abase + static_cast<uint64_t>(off[k]) * 16 + gc * 256;
-                dstv[k] = *reinterpret_cast<const u32x4*>(src);
-            }
-        };
-        // half hh of a group into slot `slot`: weight blocks give 8 bytes per half,
-        // activation blocks belong to half i/2 (encoded in bit 30 of dst)
-        auto store_half = [&](int hh, const u32x4 (&srcv)[KP]) {
-            char* base = lds + hh * S::kSlot;
-#pragma unroll
-            for (int k = 0; k < KP; ++k) {
-                if (isw[k]) {
-                    const u32x2 h = hh ? u32x2{srcv[k][2], srcv[k][3]} : u32x2{srcv[k][0], srcv[k][1]};
-                    *reinterpret_cast<u32x2*>(base + dst[k]) = h;
-                } else if ((dst[k] >> 30) == hh) {
-                    *reinterpret_cast<u32x4*>(base + (dst[k] & ((1 << 30) - 1))) = srcv[k];
-                }
-            }
-        };
-        load_group(0, v[0]);
-        load_group(1, v[1]);
-        store_half(0, v[0]);
-        __syncthreads();
-        // half step s: consumers read slot s%2; producers fill slot (s+1)%2 with
-        // half step s+1: (s even) half 1 of group s/2, (s odd) half 0 of group s/2+1.
-        for (int g = 0; g < G; g += 2) {
-            // s = 2g
-            store_half(1, v[0]);
-            load_group(g + 2, v[0]);
-            __syncthreads();
-            // s = 2g + 1
-            store_half(0, v[1]);
-            __syncthreads();
-            // s = 2g + 2
-            store_half(1, v[1]);
-            load_group(g + 3, v[1]);
-            __syncthreads();
-            // s = 2g + 3
-            store_half(0, v[0]);
-            __syncthreads();
+        for (int k = 0; k < KP; ++k)
+            if (k < KP - 1 || full) dma16(src[k] + g * gstep[k], base + dst[k]);
+    };
+    auto wait_groups = [&](int n) {
+        if (full)
+            vm_wait_groups<KP, R - 2>(n);
+        else
+            vm_wait_groups<KP - 1, R - 2>(n);
+    };
+    // prologue: groups 0 .. R-2
+    int issued = 0;
+    for (; issued < R - 1 && issued < G; ++issued) issue(issued, issued);
+    wait_groups(issued - 1);  // group 0 landed
+    dma_barrier();
+    int slot_next = issued % R;  // slot of group `issued`
+    for (int g = 0; g < G; ++g) {
+        // consumers read slot g % R; slot (g - 1) % R was released by the last barrier
+        if (issued < G) {
+            issue(issued, slot_next);
+            ++issued;
+            slot_next = slot_next + 1 == R ? 0 : slot_next + 1;
         }
+        // group g + 1 must have landed before the barrier (none left after G - 1)
+        wait_groups(g + 1 < G ? issued - g - 2 : 0);
+        dma_barrier();
     }
 }
 
-// Consumer side of one row chunk: 1 + 2*Gp barriers, matching gateup_produce.
-template <int ACT, int NC, int NP, int MT>
+// Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
+template <int ACT, int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
                                                const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
-    using S = GuShape<NC, NP>;
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid & (kWave - 1);
+    using S = GuShape<NC, NP, R>;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
     const int G = A.H >> 7;
     const NibConsts kn = nib_consts();
@@ -210,49 +240,51 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     const f16* z_g = lds_sz + kc * G;
     const f16* s_u = lds_sz + 2 * kc * G;
     const f16* z_u = lds_sz + 3 * kc * G;
-    f32x4 acc[2][MT], part[2][MT];
+    const int r = wave * 16 + col;  // row of the tile within the workgroup
+    const int fo = frag_pos(col, c) * 16;
+    f32x4 acc[2][MT];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();  // slot 0 and the scale table are ready
-    const int Gp = (G + 1) & ~1;  // producers run whole pairs of groups
-    for (int s = 0; s < 2 * Gp; ++s) {
-        const int g = s >> 1, hh = s & 1;
-        if (g < G) {
-            const char* slot = lds + hh * S::kSlot;
-            if (hh == 0) {
+    __syncthreads();  // group 0 and the scale table are ready
+    int slot = 0;
+    for (int g = 0; g < G; ++g) {
+        const char* sp = lds + slot * S::kSlot;
+        f32x4 part[2][MT];
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-            const int r = wave * 16 + col;  // row of the tile within the workgroup
+            for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        u32x4 wv[2];
+        ZeroPair zc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            wv[j] = *reinterpret_cast<const u32x4*>(sp + (wave * 2 + j) * kBlk + fo);
+            zc[j] = zero_pair((j ? z_u : z_g)[r * G + g]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f16x8 a[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                a[t] = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const ZeroPair zc = zero_pair((j ? z_u : z_g)[r * G + g]);
-                const u32x2 wv = *reinterpret_cast<const u32x2*>(slot + ((wave * 2 + j) * kWave + lane) * 8);
+                const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
 #pragma unroll
-                for (int ii = 0; ii < 2; ++ii) {
-                    const f16x8 b = nib8_minus_zero(wv[ii], zc, kn);
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        const f16x8 a = *reinterpret_cast<const f16x8*>(slot + S::kSlotW + ((t * 2 + ii) * kWave + lane) * 16);
-                        part[j][t] = mfma16x16x32(a, b, part[j][t]);
-                    }
-                }
-            }
-            if (hh == 1) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
-#pragma unroll
-                    for (int t = 0; t < MT; ++t)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
-                }
+                for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
             }
         }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
+        }
+        slot = slot + 1 == R ? 0 : slot + 1;
         __syncthreads();
     }
     // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
@@ -270,9 +302,9 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     }
 }
 
-template <int ACT, int NC, int NP>
+template <int ACT, int NC, int NP, int R>
 __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A) {
-    using S = GuShape<NC, NP>;
+    using S = GuShape<NC, NP, R>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -283,60 +315,70 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     if (M <= 0) return;
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
-    f16* lds_sz = reinterpret_cast<f16*>(lds + 2 * S::kSlot);
-    // scale / zero table of the workgroup's rows: four [kCols x G] fp16 blocks
-    // (s_gate, z_gate, s_up, z_up), each contiguous in global memory and
-    // 16-byte aligned; copied by all waves, published by the first barrier.
-    {
-        const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + c0;
-        const int64_t up0 = gate0 + A.I;
-        const int nq = S::kCols * G * 2 / 16;  // 16-byte chunks per block
-        u32x4 v[S::kSzPer];
-#pragma unroll
-        for (int k = 0; k < S::kSzPer; ++k) {
-            int i = tid + k * S::kThreads;
-            if (i >= 4 * nq) i = 0;  // clamped, never stored
-            const int b = i / nq, o = i - b * nq;
-            const f16* base = ((b & 1) ? A.gu_z : A.gu_s) + ((b & 2) ? up0 : gate0) * G;
-            v[k] = reinterpret_cast<const u32x4*>(base)[o];
-        }
-#pragma unroll
-        for (int k = 0; k < S::kSzPer; ++k) {
-            const int i = tid + k * S::kThreads;
-            if (i < 4 * nq) reinterpret_cast<u32x4*>(lds_sz)[i] = v[k];
-        }
-    }
-    // Roles split once; both loops run the same chunks with the same barrier count.
+    f16* lds_sz = reinterpret_cast<f16*>(lds + R * S::kSlot);
+    // Roles split once; both loops run the same chunks with the same barrier
+    // count (1 + G per chunk), and the ring is free after a chunk's last barrier.
     if (tid / kWave >= NC) {
         for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
             const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
             if (mrows <= 16)
-                gateup_produce<NC, NP, 1>(A, e, c0, lds, start, m0, mrows);
+                gateup_produce<NC, NP, R, 1>(A, e, c0, lds, start, m0, mrows);
             else
-                gateup_produce<NC, NP, 2>(A, e, c0, lds, start, m0, mrows);
-            __syncthreads();  // ring free for the next chunk
+                gateup_produce<NC, NP, R, 2>(A, e, c0, lds, start, m0, mrows);
         }
     } else {
+        // scale / zero table of the workgroup's rows: four [kCols x G] fp16
+        // blocks (s_gate, z_gate, s_up, z_up), each contiguous in global memory
+        // and 16-byte aligned; published by the first barrier.
+        {
+            const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + c0;
+            const int64_t up0 = gate0 + A.I;
+            const int nq = S::kCols * G * 2 / 16;  // 16-byte chunks per block
+            u32x4 v[S::kSzPer];
+#pragma unroll
+            for (int k = 0; k < S::kSzPer; ++k) {
+                int i = tid + k * NC * kWave;
+                if (i >= 4 * nq) i = 0;  // clamped, never stored
+                const int b = i / nq, o = i - b * nq;
+                const f16* base = ((b & 1) ? A.gu_z : A.gu_s) + ((b & 2) ? up0 : gate0) * G;
+                v[k] = reinterpret_cast<const u32x4*>(base)[o];
+            }
+#pragma unroll
+            for (int k = 0; k < S::kSzPer; ++k) {
+                const int i = tid + k * NC * kWave;
+                if (i < 4 * nq) reinterpret_cast<u32x4*>(lds_sz)[i] = v[k];
+            }
+        }
         for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
             const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
             if (mrows <= 16)
-                gateup_consume<ACT, NC, NP, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+                gateup_consume<ACT, NC, NP, R, 1>(A, c0, lds, lds_sz, start, m0, mrows);
             else
-                gateup_consume<ACT, NC, NP, 2>(A, c0, lds, lds_sz, start, m0, mrows);
-            __syncthreads();  // ring free for the next chunk
+                gateup_consume<ACT, NC, NP, R, 2>(A, c0, lds, lds_sz, start, m0, mrows);
         }
     }
 }
 
-template <int NC, int NP>
+template <int NC, int NP, int R>
 int launch_gateup_nc(const GuArgs& A, int64_t E, int act, hipStream_t st) {
-    using S = GuShape<NC, NP>;
+    using S = GuShape<NC, NP, R>;
     const unsigned grid = static_cast<unsigned>(E * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
+    if (lds > kLdsBytes) return KSL_ERR_SHAPE;
+    static const bool attr_set = [] {
+        // dynamic LDS beyond 64 KB: raise the per-kernel limit once
+        bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
+        ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess && ok;
+        (void)hipGetLastError();
+        return ok;
+    }();
+    (void)attr_set;
     if (act == KSL_ACT_GELU_TANH)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else if (act == KSL_ACT_SILU)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else
         return KSL_ERR_ARG;
     KSL_LAUNCH_CHECK();
@@ -360,15 +402,6 @@ struct DnArgs {
     f16* out3;
     int H, I;
 };
-
-typedef __attribute__((address_space(3))) void* lds_vptr;
-typedef __attribute__((address_space(1))) void* gbl_vptr;
-
-// Direct global -> LDS copy of one fragment block: lane L's 16 bytes land at
-// lds_block + 16*L. lds_block must be wave-uniform.
-__device__ __forceinline__ void dma16(const void* src, char* lds_block) {
-    __builtin_amdgcn_global_load_lds((gbl_vptr)(const_cast<void*>(src)), (lds_vptr)lds_block, 16, 0, 0);
-}
 
 // The activation rows of one chunk, A[g][t][i] blocks: block (g, t, i) holds,
 // for lane L = c*16 + rr, logical out2[row t*16 + rr][g*64 + c*16 + i*8 .. +8],
@@ -541,7 +574,6 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     if (!a16 || !sorted_rows || !offsets || !gu_q || !gu_s || !gu_z || !out2) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0 || topk <= 0) return KSL_ERR_SHAPE;
     if (H % 128 != 0 || I % 64 != 0 || H > 128 * kGuMaxG) return KSL_ERR_SHAPE;
-    if (E * 2 * I * (H / 2) >= (int64_t(1) << 36)) return KSL_ERR_SHAPE;  // 32-bit offsets in 16-B units
     if (reinterpret_cast<uintptr_t>(gu_q) % 16 || reinterpret_cast<uintptr_t>(a16) % 16 ||
         reinterpret_cast<uintptr_t>(gu_s) % 16 || reinterpret_cast<uintptr_t>(gu_z) % 16 ||
         reinterpret_cast<uintptr_t>(out2) % 2)
@@ -558,9 +590,13 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     A.I = static_cast<int>(I);
     A.H = static_cast<int>(H);
     // widest column block that divides I: 176 (11 consumers), 128, or 64
-    if (I % 176 == 0) return launch_gateup_nc<11, 5>(A, E, act, st);
-    if (I % 128 == 0) return launch_gateup_nc<8, 4>(A, E, act, st);
-    return launch_gateup_nc<4, 4>(A, E, act, st);
+    // (ring depth 4 where the LDS holds it: 176 columns up to H = 3712)
+    if (I % 176 == 0) {
+        if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, act, st);
+        return launch_gateup_nc<11, 5, 3>(A, E, act, st);
+    }
+    if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, act, st);
+    return launch_gateup_nc<4, 4, 4>(A, E, act, st);
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
