@@ -132,8 +132,9 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
 /* Grouped W4 gate/up GEMM with the activation fused in the epilogue.
  * Replaces _gateup_act_kernel (kernels/fused_moe_w4_v2.py:96-139).
  * out2 fp16 [T*topk, I] row per sorted slot, in the down activation order:
- * within each 64-element group, offset c*16 + i*8 + j is stored at
- * i*32 + c*8 + s(j). */
+ * the first I128 = I - I % 128 columns in the 128-element group order of a16,
+ * a trailing 64-element group (I % 128 == 64) with offset c*16 + i*8 + j
+ * stored at i*32 + c*8 + s(j). */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
                        int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);

@@ -175,6 +175,13 @@ __device__ __forceinline__ int act_store_index(int n) {
     return g0 + i * 32 + c * 8 + (perm8_store_index(o) & 7);
 }
 
+// out2 (the down GEMM's activation) uses the 128-group order over its first
+// i128 = I rounded down to a multiple of 128 columns, and the 64-group order
+// over a trailing half group (I % 128 == 64).
+__device__ __forceinline__ int out2_store_index(int n, int i128) {
+    return n < i128 ? act_store_index<128>(n) : i128 + act_store_index<64>(n - i128);
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -34,6 +34,8 @@
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
 // rows (one or two 16-row M tiles). Workgroups are remapped so that all column
 // blocks of an expert run on the same XCD (shared L2 for its activations).
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "ksl_common.h"
@@ -42,6 +44,10 @@ namespace ksl {
 namespace {
 
 constexpr int kXcds = 8;
+
+// Index of the calling wave in its workgroup, in a scalar register (branches
+// on it are uniform).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
 
 // blockIdx.x -> logical tile, placing consecutive logical tiles on one XCD
 // (workgroups are dispatched round-robin over the XCDs).
@@ -166,7 +172,7 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
     constexpr int NB = 2 * NC + 4 * MT;
     constexpr int KP = (NB + NP - 1) / NP;
     const int lane = threadIdx.x & (kWave - 1);
-    const int p = threadIdx.x / kWave - NC;
+    const int p = wave_id() - NC;
     // row-major fetch: lanes 4r .. 4r+3 cover the 64 bytes of block row r
     // (4 rows per 256 B), chunk order swizzled per row (frag_pos)
     const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
@@ -230,7 +236,7 @@ template <int ACT, int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
                                                const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
     using S = GuShape<NC, NP, R>;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
     const int G = A.H >> 7;
@@ -289,7 +295,7 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     }
     // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
     {
-        const int sc = act_store_index<64>(c0 + wave * 16 + col);  // out2 is the down GEMM's activation
+        const int sc = out2_store_index(c0 + wave * 16 + col, A.I & ~127);  // out2 is the down GEMM's activation
         f16* o = A.out2 + static_cast<int64_t>(start + m0) * A.I + sc;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -318,7 +324,7 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     f16* lds_sz = reinterpret_cast<f16*>(lds + R * S::kSlot);
     // Roles split once; both loops run the same chunks with the same barrier
     // count (1 + G per chunk), and the ring is free after a chunk's last barrier.
-    if (tid / kWave >= NC) {
+    if (wave_id() >= NC) {
         for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
             const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
             if (mrows <= 16)
@@ -359,21 +365,41 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     }
 }
 
+// Dynamic LDS beyond 64 KB: raise a kernel's limit (called once per kernel).
+bool set_max_lds(const void* fn) {
+    const bool ok = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
+    (void)hipGetLastError();
+    return ok;
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cache[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 template <int NC, int NP, int R>
 int launch_gateup_nc(const GuArgs& A, int64_t E, int act, hipStream_t st) {
     using S = GuShape<NC, NP, R>;
     const unsigned grid = static_cast<unsigned>(E * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
     if (lds > kLdsBytes) return KSL_ERR_SHAPE;
-    static const bool attr_set = [] {
-        // dynamic LDS beyond 64 KB: raise the per-kernel limit once
-        bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
-        ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess && ok;
-        (void)hipGetLastError();
-        return ok;
-    }();
+    static const bool attr_set = set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>)) &&
+                                 set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>));
     (void)attr_set;
     if (act == KSL_ACT_GELU_TANH)
         hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
@@ -386,12 +412,26 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int act, hipStream_t st) {
 }
 
 // --------------------------------------------------------------------- down
-constexpr int kDnWaves = 4;
-constexpr int kDnTiles = 2;                          // 16-column tiles of H per wave
-constexpr int kDnWgCols = 16 * kDnTiles * kDnWaves;  // 128 columns of H per workgroup
-constexpr int kDnThreads = kDnWaves * kWave;         // 256
-constexpr int kDnBlock = kWave * 16;                 // one LDS fragment block: 64 lanes x 16 B
-constexpr int kDnSzPer = (2 * kDnWgCols * 16 / 2 + kDnThreads - 1) / kDnThreads;  // I <= 1024
+// Register-streamed kernel. A workgroup of kDnWaves waves owns one expert and
+// a range of its output columns (the expert's H columns split over
+// ceil(#CUs / E) workgroups); the expert's activation rows (out2, up to 32 per
+// chunk) and the scale / zero rows of the workgroup's columns are copied into
+// LDS once (direct global->LDS loads), so each activation row is read once
+// per workgroup. Every wave then walks its 16-column tiles (tiles w, w+11, ...)
+// with the weights in registers, double buffered: the next tile's 16 rows x
+// I/2 bytes are loaded while the current tile is decoded and multiplied, and
+// all waves do MFMA and nibble decoding (down's decode, with the scale folded
+// in, costs as much VALU time as the bytes take to stream).
+//
+// K mapping: one 16-byte load per lane and 128-K block, lane (col, c) holding
+// row col, nibbles 32c .. 32c+31 of the block: MFMA step i takes nibbles
+// 32c + 8i .. +8, the 128-group activation order (out2_store_index); the scale
+// group of lane group c is 2*g2 + c/2. A trailing 64-K group (I % 128 == 64)
+// takes an 8-byte load, the 64-group order. B = fp16((q - z) * s), the
+// reference's own dequantised weight (kernels/fused_moe_w4_v2.py:172-175).
+constexpr int kDnWaves = 11;
+constexpr int kDnThreads = kDnWaves * kWave;
+constexpr int kDnMaxG = 16;  // I <= 1024
 
 struct DnArgs {
     const f16* out2;
@@ -400,170 +440,240 @@ struct DnArgs {
     const f16* dn_s;
     const f16* dn_z;
     f16* out3;
-    int H, I;
+    int H, I, nsplit, tpw;  // tpw: 16-column tiles per workgroup
 };
 
-// The activation rows of one chunk, A[g][t][i] blocks: block (g, t, i) holds,
-// for lane L = c*16 + rr, logical out2[row t*16 + rr][g*64 + c*16 + i*8 .. +8],
-// stored at g*64 + i*32 + c*8 (act_store_index<64>).
-template <int G>
-__device__ __forceinline__ void down_stage_a(const DnArgs& A, char* lds_a, int start, int m0, int mrows,
-                                             int mt) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int rr = lane & 15, c = lane >> 4;
-    const int nblk = G * mt * 2;
-    for (int b = wave; b < nblk; b += kDnWaves) {
-        const int i = b & 1;
-        const int t = (b >> 1) % mt;
-        const int g = (b >> 1) / mt;
-        int r = t * 16 + rr;
-        if (r >= mrows) r = mrows - 1;
-        const f16* src = A.out2 + static_cast<int64_t>(start + m0 + r) * A.I + g * 64 + i * 32 + c * 8;
-        dma16(src, lds_a + ((g * kMaxMt + t) * 2 + i) * kDnBlock);
+// LDS: activation blocks [kMaxMt][2G] (1 KB each, frag_pos order), then the
+// s rows and the z rows ([nrows][G] fp16 each) of the workgroup's columns.
+inline size_t dn_lds_bytes(int G, int nrows) {
+    return static_cast<size_t>(kMaxMt) * 2 * G * kBlk + static_cast<size_t>(nrows) * G * 4;
+}
+
+template <int G2, bool TAIL>
+struct DnW {
+    u32x4 q[G2];
+    u32x2 t[TAIL ? 1 : 0];
+};
+
+// A tile's weights: G2 16-byte loads and, with TAIL, one 8-byte load. Issued
+// as asm so that the compiler's conservative wait at the tile loop's head
+// (vmcnt(0), which would drain the next tile's prefetch) is not inserted; the
+// waits are explicit (dn_wait_w), the compiler-placed ones can only wait more.
+// The compiler takes the registers as written at the asm: nothing may copy
+// them before dn_wait_w, so a buffer enters the tile loop only once complete
+// and is otherwise loaded and used inside one loop iteration pair (checked in
+// the generated code: no register copies of a loading buffer).
+template <int G2, bool TAIL>
+__device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* rowp, int c) {
+    const uint8_t* p = rowp + c * 16;
+#pragma unroll
+    for (int g2 = 0; g2 < G2; ++g2)
+        asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w.q[g2]) : "v"(p), "i"(g2 * 64) : "memory");
+    if constexpr (TAIL) {
+        const uint8_t* pt = rowp + G2 * 64 + c * 8;
+        asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
     }
 }
 
-template <int G, int MT>
-__device__ __forceinline__ void down_chunk(const DnArgs& A, const u32x2 (&w)[kDnTiles][G],
-                                           const char* __restrict__ lds_a, const f16* __restrict__ lds_s,
-                                           const f16* __restrict__ lds_z, int n0w, int wrow0, int start,
-                                           int m0, int mrows) {
-    // Down keeps one accumulator chain per tile: the scale is folded into the
-    // B operand, b = fp16((q - z) * s), the reference's own dequantised weight.
-    const int lane = threadIdx.x & (kWave - 1);
-    const int col = lane & 15, c = lane >> 4;
-    const NibConsts kn = nib_consts();
-    f32x4 acc[kDnTiles][MT];
+// Wait until the loads of w have landed, N memory operations issued after
+// them allowed in flight; the empty asm orders every use of w after the wait.
+template <int N, int G2, bool TAIL>
+__device__ __forceinline__ void dn_wait_w(DnW<G2, TAIL>& w) {
+    vm_wait<N>();
 #pragma unroll
-    for (int j = 0; j < kDnTiles; ++j)
+    for (int g2 = 0; g2 < G2; ++g2) asm volatile("" : "+v"(w.q[g2]));
+    if constexpr (TAIL) asm volatile("" : "+v"(w.t[0]));
+}
+
+template <int G2, bool TAIL, int MT>
+__device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[kMaxMt], const char* __restrict__ a_lds,
+                                        const f16* __restrict__ srow, const f16* __restrict__ zrow, int c, int fo,
+                                        const NibConsts& kn) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
 #pragma unroll
-        for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g2 = 0; g2 < G2; ++g2) {
+        const int grp = 2 * g2 + (c >> 1);
+        const f16 sv = srow[grp];
+        const ZeroPair zc = zero_pair(zrow[grp]);
+        // decode here, not where the load lands (decoded nibbles take 4x the registers)
+        u32x4 wq = w.q[g2];
+        asm volatile("" : "+v"(wq));
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        f16x2 sc[kDnTiles];
-        ZeroPair zc[kDnTiles];
+        for (int i = 0; i < 4; ++i) {
+            const f16x8 b = nib8_dequant(wq[i], zc, f16x2{sv, sv}, kn);
 #pragma unroll
-        for (int j = 0; j < kDnTiles; ++j) {
-            const int r = wrow0 + j * 16 + col;
-            const f16 sv = lds_s[r * G + g];
-            sc[j] = f16x2{sv, sv};
-            zc[j] = zero_pair(lds_z[r * G + g]);
+            for (int t = 0; t < MT; ++t) {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + g2 * 4 + i) * kBlk + fo);
+                acc[t] = mfma16x16x32(a, b, acc[t]);
+            }
         }
+        // one 128-K block at a time: the other waves hide its LDS latency, and
+        // hoisting every block's operands would exceed the register budget
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (TAIL) {
+        const f16 sv = srow[2 * G2];
+        const ZeroPair zc = zero_pair(zrow[2 * G2]);
+        u32x2 wt = w.t[0];
+        asm volatile("" : "+v"(wt));
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            f16x8 a[MT];
+            const f16x8 b = nib8_dequant(wt[i], zc, f16x2{sv, sv}, kn);
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
-                a[t] = *reinterpret_cast<const f16x8*>(lds_a + ((g * kMaxMt + t) * 2 + i) * kDnBlock + lane * 16);
-#pragma unroll
-            for (int j = 0; j < kDnTiles; ++j) {
-                const f16x8 b = nib8_dequant(w[j][g][i], zc[j], sc[j], kn);
-#pragma unroll
-                for (int t = 0; t < MT; ++t) acc[j][t] = mfma16x16x32(a[t], b, acc[j][t]);
+            for (int t = 0; t < MT; ++t) {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + G2 * 4 + i) * kBlk + fo);
+                acc[t] = mfma16x16x32(a, b, acc[t]);
             }
         }
     }
-    f16* o = A.out3 + static_cast<int64_t>(start + m0) * A.H + n0w + col;
-#pragma unroll
-    for (int j = 0; j < kDnTiles; ++j)
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = t * 16 + 4 * c + r;
-                if (row < mrows) o[static_cast<int64_t>(row) * A.H + j * 16] = static_cast<f16>(acc[j][t][r]);
-            }
 }
 
-// One workgroup: expert e, 128 columns of H. All of a wave's weights (2 tiles x
-// G groups x 8 bytes per lane) are loaded once into registers and reused for
-// every 32-row chunk of the expert; the chunk's activations go to LDS by
-// direct global->LDS loads.
-template <int G>
-__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(3))) void down_kernel(DnArgs A) {
+// Activation blocks of one chunk into LDS: block b = t*2G + bb, bb < 4*G2 the
+// 128-K block bb/4, step bb%4; else tail step bb - 4*G2. Rows fetched
+// row-major (frag_pos). Issued by every wave, round-robin.
+template <int G2, bool TAIL>
+__device__ __forceinline__ void dn_stage_a(const DnArgs& A, char* a_lds, int start, int m0, int mrows, int mt,
+                                           int wave, int rr, int ch) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
+    for (int b = wave; b < mt * 2 * G; b += kDnWaves) {
+        const int t = b / (2 * G), bb = b - t * 2 * G;
+        const int off = bb < 4 * G2 ? (bb >> 2) * 128 + (bb & 3) * 32 : G2 * 128 + (bb - 4 * G2) * 32;
+        int r = t * 16 + rr;
+        if (r >= mrows) r = mrows - 1;  // rows past the expert's last: loaded, never stored
+        dma16(A.out2 + static_cast<int64_t>(start + m0 + r) * A.I + off + ch * 8, a_lds + b * kBlk);
+    }
+}
+
+// Buffer resource over `bytes` bytes at p (gfx9 raw buffer: stride 0, byte
+// offsets; a store at an offset past the end is dropped by the hardware).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
+}
+constexpr uint32_t kDropOffset = 0x80000000u;
+
+// One tile: MT M tiles x 16 columns. The stores have no branches (rows past
+// the chunk, or a repeated tile, take an out-of-range offset), so every wave
+// issues the same number of memory operations per tile and the waits on the
+// prefetched weights are exact.
+template <int G2, bool TAIL, int MT>
+__device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a_lds, const f16* s_lds,
+                                           const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int tile,
+                                           int colw, bool valid, int mrows, int col, int c, int fo,
+                                           const NibConsts& kn) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
+    f32x4 acc[kMaxMt];
+#pragma unroll
+    for (int t = 0; t < kMaxMt; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rl = tile * 16 + col;  // row of dn within the workgroup's columns
+    dn_tile<G2, TAIL, MT>(w, acc, a_lds, s_lds + rl * G, z_lds + rl * G, c, fo, kn);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int row = t * 16 + 4 * c + q;
+            const uint32_t off = valid && row < mrows ? static_cast<uint32_t>((row * H + colw + tile * 16 + col) * 2)
+                                                      : kDropOffset;
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16>(acc[t][q])),
+                                                  out, off, 0, 0);
+        }
+}
+
+// A wave's tiles of one chunk: tiles wave + k*kDnWaves, k < nmine, weights of
+// tile k+1 loaded while tile k is computed. Loads are unconditional (past the
+// last tile they repeat it: an L2 hit), a repeated tile's stores are dropped,
+// so between a buffer's loads and its use exactly the other buffer's loads and
+// one tile's 4*MT stores are issued (on entry w0 has landed already).
+template <int G2, bool TAIL, int MT>
+__device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, const uint8_t* wrow, int rb,
+                                         int nmine, int wave, const char* a_lds, const f16* s_lds,
+                                         const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int colw, int mrows,
+                                         int col, int c, int fo, const NibConsts& kn) {
+    constexpr int kAfter = G2 + (TAIL ? 1 : 0) + 4 * MT;
+    for (int k = 0; k < nmine; k += 2) {
+        const int k1 = k + 1 < nmine ? k + 1 : nmine - 1;
+        const int k2 = k + 2 < nmine ? k + 2 : nmine - 1;
+        dn_load_w<G2, TAIL>(w1, wrow + static_cast<int64_t>(wave + k1 * kDnWaves) * 16 * rb, c);
+        dn_wait_w<kAfter>(w0);
+        dn_do_tile<G2, TAIL, MT>(w0, a_lds, s_lds, z_lds, out, H, wave + k * kDnWaves, colw, true, mrows, col, c,
+                                 fo, kn);
+        dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave + k2 * kDnWaves) * 16 * rb, c);
+        dn_wait_w<kAfter>(w1);
+        dn_do_tile<G2, TAIL, MT>(w1, a_lds, s_lds, z_lds, out, H, wave + k1 * kDnWaves, colw, k + 1 < nmine, mrows,
+                                 col, c, fo, kn);
+    }
+}
+
+template <int G2, bool TAIL>
+__global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const int nb_per_e = (A.H + kDnWgCols - 1) / kDnWgCols;
-    const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int e = tile / nb_per_e;
-    const int nb = tile - e * nb_per_e;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int e = bid / A.nsplit;
+    const int h = bid - e * A.nsplit;
     const int start = A.offsets[e];
     const int M = A.offsets[e + 1] - start;
-    if (M <= 0) return;
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid & (kWave - 1);
+    const int col0 = h * A.tpw * 16;
+    const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
+    if (M <= 0 || ncols <= 0) return;
+    const int ntiles = ncols >> 4;
+    const int wave = wave_id();
+    const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
-    const int nbase = nb * kDnWgCols;                                     // first column of the workgroup
-    const int nrows = A.H - nbase < kDnWgCols ? A.H - nbase : kDnWgCols;  // multiple of 64
-    const int n0w = nbase + wave * 16 * kDnTiles;                         // first column of this wave
-    const bool wave_active = n0w < A.H;
-
-    char* lds_a = lds;                                                      // [G][kMaxMt][2] blocks
-    f16* lds_s = reinterpret_cast<f16*>(lds + G * kMaxMt * 2 * kDnBlock);  // [128][G]
-    f16* lds_z = lds_s + kDnWgCols * G;
-
-    // 1. scales / zeros of the workgroup's rows into registers
-    const int64_t row0 = static_cast<int64_t>(e) * A.H + nbase;
-    const int nd = nrows * G / 2;  // dwords per block; row0 even, so 4-byte aligned
-    uint32_t szs[kDnSzPer], szz[kDnSzPer];
-#pragma unroll
-    for (int k = 0; k < kDnSzPer; ++k) {
-        const int i = tid + k * kDnThreads < nd ? tid + k * kDnThreads : 0;  // clamped, never stored
-        szs[k] = reinterpret_cast<const uint32_t*>(A.dn_s + row0 * G)[i];
-        szz[k] = reinterpret_cast<const uint32_t*>(A.dn_z + row0 * G)[i];
-    }
-    // 2. all weights of this wave
-    u32x2 w[kDnTiles][G];
+    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int fo = frag_pos(col, c) * 16;
+    const NibConsts kn = nib_consts();
+    char* a_lds = lds;
+    f16* s_lds = reinterpret_cast<f16*>(lds + kMaxMt * 2 * G * kBlk);
+    f16* z_lds = s_lds + ncols * G;
+    const int64_t row0 = static_cast<int64_t>(e) * A.H + col0;  // first dn row of the workgroup
+    const int rb = A.I >> 1;
+    const uint8_t* wrow = A.dn_q + (row0 + col) * rb;  // this lane's row in tile 0
+    // 1. scale / zero rows and the first chunk's activations into LDS
     {
-        // an inactive wave (H % 128 == 64, last block) loads the block's first rows instead
-        const int wr = wave_active ? wave * 16 * kDnTiles : 0;
-#pragma unroll
-        for (int j = 0; j < kDnTiles; ++j) {
-            const uint8_t* wp = A.dn_q + (row0 + wr + j * 16 + col) * (A.I >> 1) + c * 8;
-#pragma unroll
-            for (int g = 0; g < G; ++g) w[j][g] = *reinterpret_cast<const u32x2*>(wp + g * 32);
+        const int nq = ncols * G / 8;  // 16-byte chunks per block
+        const char* ssrc = reinterpret_cast<const char*>(A.dn_s + row0 * G);
+        const char* zsrc = reinterpret_cast<const char*>(A.dn_z + row0 * G);
+        for (int q0 = wave * kWave; q0 < 2 * nq; q0 += kDnWaves * kWave) {
+            const int q = q0 + lane;
+            if (q < 2 * nq) dma16(q < nq ? ssrc + q * 16 : zsrc + (q - nq) * 16, reinterpret_cast<char*>(s_lds) + q0 * 16);
         }
-    }
-    // 3. activations of the first chunk, straight into LDS
-    {
         const int mrows = M < 16 * kMaxMt ? M : 16 * kMaxMt;
-        down_stage_a<G>(A, lds_a, start, 0, mrows, mrows <= 16 ? 1 : 2);
+        dn_stage_a<G2, TAIL>(A, a_lds, start, 0, mrows, mrows > 16 ? 2 : 1, wave, rr, ch);
     }
-#pragma unroll
-    for (int k = 0; k < kDnSzPer; ++k) {
-        const int i = tid + k * kDnThreads;
-        if (i < nd) {
-            reinterpret_cast<uint32_t*>(lds_s)[i] = szs[k];
-            reinterpret_cast<uint32_t*>(lds_z)[i] = szz[k];
-        }
-    }
-    // every wave's direct-to-LDS loads must have landed before any wave reads
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
+    // 2. the first tile's weights, then wait for the LDS copies only
+    DnW<G2, TAIL> w0, w1;
+    if (wave < ntiles) dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, c);
+    vm_wait<0>();
+    dma_barrier();
+    const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDnWaves + 1 : 0;
     for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
         const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
         if (m0 > 0) {
-            __syncthreads();  // previous chunk's LDS reads done
-            down_stage_a<G>(A, lds_a, start, m0, mrows, mrows <= 16 ? 1 : 2);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+            __syncthreads();  // every wave is done with the previous chunk's activations
+            dn_stage_a<G2, TAIL>(A, a_lds, start, m0, mrows, mrows > 16 ? 2 : 1, wave, rr, ch);
+            if (wave < ntiles) dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, c);
+            vm_wait<0>();
+            dma_barrier();
         }
-        if (wave_active) {
-            // The nibble decode of w does not depend on the chunk: without this
-            // (empty) redefinition it is hoisted out of the loop for all G
-            // groups and keeps ~4x the weight registers live.
-#pragma unroll
-            for (int j = 0; j < kDnTiles; ++j)
-#pragma unroll
-                for (int g = 0; g < G; ++g) asm volatile("" : "+v"(w[j][g]));
-            if (mrows <= 16)
-                down_chunk<G, 1>(A, w, lds_a, lds_s, lds_z, n0w, wave * 16 * kDnTiles, start, m0, mrows);
-            else
-                down_chunk<G, 2>(A, w, lds_a, lds_s, lds_z, n0w, wave * 16 * kDnTiles, start, m0, mrows);
-        }
+        const __amdgpu_buffer_rsrc_t out =
+            raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
+        if (mrows > 16)
+            dn_tiles<G2, TAIL, 2>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
+                                  fo, kn);
+        else
+            dn_tiles<G2, TAIL, 1>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
+                                  fo, kn);
     }
+    vm_wait<0>();  // the last (repeated) prefetch lands before the wave ends
+}
+
+template <int G2, bool TAIL>
+int launch_down_g(const DnArgs& A, unsigned grid, size_t lds, hipStream_t st) {
+    static const bool attr = set_max_lds(reinterpret_cast<const void*>(&down_kernel<G2, TAIL>));
+    (void)attr;
+    hipLaunchKernelGGL((down_kernel<G2, TAIL>), dim3(grid), dim3(kDnThreads), lds, st, A);
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }
 
 }  // namespace
@@ -603,10 +713,9 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st) {
     if (!out2 || !offsets || !dn_q || !dn_s || !dn_z || !out3) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
-    if (H % 64 != 0 || I % 64 != 0 || I > 1024) return KSL_ERR_SHAPE;
-    if (E * H * (I / 2) >= (int64_t(1) << 40)) return KSL_ERR_SHAPE;
-    if (reinterpret_cast<uintptr_t>(dn_q) % 8 || reinterpret_cast<uintptr_t>(out2) % 16 ||
-        reinterpret_cast<uintptr_t>(dn_s) % 4 || reinterpret_cast<uintptr_t>(dn_z) % 4 ||
+    if (H % 64 != 0 || I % 64 != 0 || I > 64 * kDnMaxG || H >= (1 << 24) || E >= (1 << 24)) return KSL_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(out2) % 16 ||
+        reinterpret_cast<uintptr_t>(dn_s) % 16 || reinterpret_cast<uintptr_t>(dn_z) % 16 ||
         reinterpret_cast<uintptr_t>(out3) % 2)
         return KSL_ERR_ALIGN;
     DnArgs A;
@@ -619,19 +728,28 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     A.H = static_cast<int>(H);
     A.I = static_cast<int>(I);
     const int G = static_cast<int>(I / 64);
-    const unsigned grid = static_cast<unsigned>(E * ((H + kDnWgCols - 1) / kDnWgCols));
-    const size_t lds = static_cast<size_t>(G) * kMaxMt * 2 * kDnBlock + 2 * kDnWgCols * G * sizeof(f16);
+    // columns per workgroup: enough workgroups to fill the CUs, few enough
+    // columns that their scale / zero rows fit in LDS beside the activations
+    const int64_t te = H / 16;  // 16-column tiles per expert
+    const int64_t max_tiles = static_cast<int64_t>((kLdsBytes - dn_lds_bytes(G, 0)) / (static_cast<size_t>(16) * G * 4));
+    int64_t nsplit = std::max<int64_t>((device_cus() + E - 1) / E, (te + max_tiles - 1) / max_tiles);
+    nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, te));
+    const int64_t tpw = (te + nsplit - 1) / nsplit;
+    nsplit = (te + tpw - 1) / tpw;
+    A.tpw = static_cast<int>(tpw);
+    A.nsplit = static_cast<int>(nsplit);
+    const int64_t grid = E * nsplit;
+    if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    const size_t lds = dn_lds_bytes(G, static_cast<int>(tpw * 16));
     switch (G) {
 #define KSL_DN_CASE(GG) \
-    case GG: hipLaunchKernelGGL(down_kernel<GG>, dim3(grid), dim3(kDnThreads), lds, st, A); break;
+    case GG: return launch_down_g<GG / 2, (GG % 2) != 0>(A, static_cast<unsigned>(grid), lds, st);
         KSL_DN_CASE(1) KSL_DN_CASE(2) KSL_DN_CASE(3) KSL_DN_CASE(4) KSL_DN_CASE(5) KSL_DN_CASE(6)
         KSL_DN_CASE(7) KSL_DN_CASE(8) KSL_DN_CASE(9) KSL_DN_CASE(10) KSL_DN_CASE(11) KSL_DN_CASE(12)
         KSL_DN_CASE(13) KSL_DN_CASE(14) KSL_DN_CASE(15) KSL_DN_CASE(16)
 #undef KSL_DN_CASE
         default: return KSL_ERR_SHAPE;
     }
-    KSL_LAUNCH_CHECK();
-    return KSL_OK;
 }
 
 }  // namespace ksl

@@ -55,3 +55,12 @@ def act_unperm(a: np.ndarray, gs: int) -> np.ndarray:
     sj = np.where(j < 4, 2 * j, 2 * (j - 4) + 1)
     store = g0 + i * 32 + c * 8 + sj
     return a[..., store]
+
+
+def out2_unperm(a: np.ndarray, I: int) -> np.ndarray:
+    """Undo the out2 storage order: 128-element groups over the first I - I % 128
+    columns, a 64-element group over the rest."""
+    i128 = I - I % 128
+    if i128 == I:
+        return act_unperm(a, 128)
+    return np.concatenate([act_unperm(a[..., :i128], 128), act_unperm(a[..., i128:], 64)], axis=-1)

@@ -18,7 +18,7 @@ import torch
 
 from oracle import moe_oracle as mo
 from oracle import oracle_c
-from tests._helpers import MOE_MAX_TOL, MOE_MEAN_TOL, act_unperm, bf16_bits, f16_bits, norm_err
+from tests._helpers import MOE_MAX_TOL, MOE_MEAN_TOL, act_unperm, bf16_bits, f16_bits, norm_err, out2_unperm
 from tests.conftest import load_mod, load_pkg
 
 pytestmark = pytest.mark.gpu
@@ -148,7 +148,7 @@ def test_gateup_and_down_stages(gpu, act, T, tk, E, H, I, seed):
     _, ref_out2, _ = mo.moe_forward_per_expert(hidden.float().numpy(), gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
                                                 ids.numpy(), np.ones((T, tk), np.float32), ACTS[act])
     inv_np = _np(inv).astype(np.int64)
-    got_out2 = act_unperm(_np(out2), 64)[inv_np]        # back to expanded-row order
+    got_out2 = out2_unperm(_np(out2), I)[inv_np]        # back to expanded-row order
     mx, mean = norm_err(got_out2.astype(np.float32), ref_out2.astype(np.float32))
     print(f"gate/up {act} T={T} E={E} H={H} I={I}: norm max {mx:.2e} mean {mean:.2e}")
     assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
