@@ -77,6 +77,35 @@ template <> __device__ __forceinline__ void load8<KSL_DTYPE_F32>(const void* p, 
     }
 }
 
+// 8 consecutive elements kept as loaded (4 registers for 2-byte types): rows
+// held across a reduction stay in this form and are widened on use.
+template <int DT> struct Raw8 { u32x4 q[DT == KSL_DTYPE_F32 ? 2 : 1]; };
+template <int DT> __device__ __forceinline__ Raw8<DT> raw_load8(const void* p) {
+    Raw8<DT> r;
+#pragma unroll
+    for (int i = 0; i < (DT == KSL_DTYPE_F32 ? 2 : 1); ++i) r.q[i] = reinterpret_cast<const u32x4*>(p)[i];
+    return r;
+}
+template <int DT> __device__ __forceinline__ void raw_unpack8(const Raw8<DT>& r, float (&v)[8]) {
+    if constexpr (DT == KSL_DTYPE_BF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(r.q[0][i] << 16);
+            v[2 * i + 1] = __uint_as_float(r.q[0][i] & 0xFFFF0000u);
+        }
+    } else if constexpr (DT == KSL_DTYPE_F16) {
+        const f16x8 h = __builtin_bit_cast(f16x8, r.q[0]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(h[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __uint_as_float(r.q[0][i]);
+            v[4 + i] = __uint_as_float(r.q[1][i]);
+        }
+    }
+}
+
 // Store 8 consecutive values (already rounded as the caller wants).
 template <int DT> __device__ __forceinline__ void store8(void* p, const float (&v)[8]);
 template <> __device__ __forceinline__ void store8<KSL_DTYPE_BF16>(void* p, const float (&v)[8]) {
@@ -189,42 +218,56 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 // ---- RMSNorm of one row, shared by the standalone kernel and the fused layer
 // prep (kernels/fused_rmsnorm.py:10-21). The row is split over LPR = 1 << lpr_log2
 // lanes; lane sl owns 8 consecutive columns per step, NSTEP steps, so
-// c0(s) = s*8*LPR + sl*8. x and w are loaded up front (one round trip), the
-// fp32 sum of squares is reduced over the LPR lanes by a fixed xor tree, and
-// out[s][j] receives bf16(x * (1/sqrt(ms)) [* w]) as a float.
-template <int XD, int WD, int NSTEP, bool HAS_W>
+// c0(s) = s*8*LPR + sl*8. x and w are loaded up front (one round trip, kept
+// as loaded), the fp32 sum of squares is reduced over the LPR lanes by a fixed
+// xor tree, and emit(s, c0, o) receives o[j] = bf16(x * (1/sqrt(ms)) [* w]) as
+// floats for every step with c0 < cols.
+template <int XD, int WD, int NSTEP, bool HAS_W, typename Emit>
 __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__ xr,
                                         const typename Elem<WD>::T* __restrict__ w, int cols, float eps,
-                                        int sl, int lpr_log2, bool row_ok, float (&out)[NSTEP][8]) {
+                                        int sl, int lpr_log2, bool row_ok, Emit&& emit) {
     const int stride_cols = 8 << lpr_log2;
-    float wf[NSTEP][8];
-    float ss = 0.0f;
+    Raw8<XD> xv[NSTEP];
+    Raw8<WD> wv[HAS_W ? NSTEP : 1];
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
         const int c0 = s * stride_cols + sl * 8;
         if (row_ok && c0 < cols) {
-            load8<XD>(xr + c0, out[s]);
-            if (HAS_W) load8<WD>(w + c0, wf[s]);
+            xv[s] = raw_load8<XD>(xr + c0);
+            if constexpr (HAS_W) wv[s] = raw_load8<WD>(w + c0);
         } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) out[s][j] = 0.0f;
+            xv[s] = Raw8<XD>{};  // zeros
         }
     }
+    float ss = 0.0f;
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s)
+    for (int s = 0; s < NSTEP; ++s) {
+        float xf[8];
+        raw_unpack8<XD>(xv[s], xf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(out[s][j], out[s][j], ss);
+        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(xf[j], xf[j], ss);
+    }
     for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
     const float ms = ss / static_cast<float>(cols) + eps;
     const float r = 1.0f / __builtin_sqrtf(ms);
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s)
+    for (int s = 0; s < NSTEP; ++s) {
+        const int c0 = s * stride_cols + sl * 8;
+        if (c0 >= cols) continue;
+        float xf[8], wf[8], o[8];
+        // widen again here: keeping the first pass's floats live doubles the registers
+#pragma unroll
+        for (int i = 0; i < (XD == KSL_DTYPE_F32 ? 2 : 1); ++i) asm volatile("" : "+v"(xv[s].q[i]));
+        raw_unpack8<XD>(xv[s], xf);
+        if constexpr (HAS_W) raw_unpack8<WD>(wv[s], wf);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float o = out[s][j] * r;
-            if (HAS_W) o = o * wf[s][j];
-            out[s][j] = bf16_bits_to_f32(f32_to_bf16_bits(o));  // the reference stores bf16
+            float t = xf[j] * r;
+            if constexpr (HAS_W) t = t * wf[j];
+            o[j] = bf16_bits_to_f32(f32_to_bf16_bits(t));  // the reference stores bf16
         }
+        emit(s, c0, o);
+    }
 }
 
 }  // namespace ksl

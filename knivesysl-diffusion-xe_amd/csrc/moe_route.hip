@@ -133,24 +133,20 @@ __global__ __launch_bounds__(kRouteThreads) void route_norm_kernel(
     const int wave = threadIdx.x / kWave;
     const int64_t nworkers = static_cast<int64_t>(gridDim.x - 1) * kRouteWaves;
     for (int64_t row = static_cast<int64_t>(blockIdx.x - 1) * kRouteWaves + wave; row < T; row += nworkers) {
-        float v[NSTEP][8];
-        rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true, v);
-#pragma unroll
-        for (int s = 0; s < NSTEP; ++s) {
-            const int c0 = s * 512 + lane * 8;
-            if (c0 < H) {
-                f16x8 o;
-                o[0] = static_cast<f16>(v[s][0]);
-                o[1] = static_cast<f16>(v[s][4]);
-                o[2] = static_cast<f16>(v[s][1]);
-                o[3] = static_cast<f16>(v[s][5]);
-                o[4] = static_cast<f16>(v[s][2]);
-                o[5] = static_cast<f16>(v[s][6]);
-                o[6] = static_cast<f16>(v[s][3]);
-                o[7] = static_cast<f16>(v[s][7]);
-                *reinterpret_cast<f16x8*>(a16 + row * H + act_store_index<128>(c0)) = o;
-            }
-        }
+        f16* arow = a16 + row * H;
+        rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true,
+                                      [&](int, int c0, const float (&v)[8]) {
+                                          f16x8 o;
+                                          o[0] = static_cast<f16>(v[0]);
+                                          o[1] = static_cast<f16>(v[4]);
+                                          o[2] = static_cast<f16>(v[1]);
+                                          o[3] = static_cast<f16>(v[5]);
+                                          o[4] = static_cast<f16>(v[2]);
+                                          o[5] = static_cast<f16>(v[6]);
+                                          o[6] = static_cast<f16>(v[3]);
+                                          o[7] = static_cast<f16>(v[7]);
+                                          *reinterpret_cast<f16x8*>(arow + act_store_index<128>(c0)) = o;
+                                      });
     }
 }
 

@@ -42,15 +42,11 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_vec_kernel(
 
     constexpr int NS1 = NSTEP > 0 ? NSTEP : 1;
     if (NSTEP > 0) {
-        float v[NS1][8];
-        rms_row<XD, WD, NS1, HAS_W>(x + (row_ok ? row : 0) * xs, w, cols, eps, sl, lpr_log2, row_ok, v);
-        if (!row_ok) return;
-        YT* yr = y + row * ys;
-#pragma unroll
-        for (int s = 0; s < NS1; ++s) {
-            const int c0 = s * stride_cols + sl * 8;
-            if (c0 < cols) store8<YD>(yr + c0, v[s]);
-        }
+        YT* yr = y + (row_ok ? row : 0) * ys;
+        rms_row<XD, WD, NS1, HAS_W>(x + (row_ok ? row : 0) * xs, w, cols, eps, sl, lpr_log2, row_ok,
+                                    [&](int, int c0, const float (&o)[8]) {
+                                        if (row_ok) store8<YD>(yr + c0, o);
+                                    });
         return;
     }
     // long rows: two passes over x

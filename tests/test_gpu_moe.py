@@ -104,6 +104,36 @@ def test_route_compact_and_activation_copy(gpu):
     assert np.array_equal(act_unperm(f16_bits(a16.cpu()), 128), f16_bits(ref16))
 
 
+ROUTE_CASES = [
+    # (T, tk, E, seed, dropped)  T*tk <= 4096: one wave per expert; above: one workgroup
+    (256, 8, 128, 23, False),
+    (37, 3, 8, 24, True),
+    (300, 2, 512, 25, True),
+    (1, 8, 128, 26, False),
+    (512, 8, 128, 27, True),
+    (600, 8, 128, 28, True),
+]
+
+
+@pytest.mark.parametrize("T,tk,E,seed,dropped", ROUTE_CASES)
+def test_route_compact_bit_exact(gpu, T, tk, E, seed, dropped):
+    wl = load_mod("workloads")
+    ids, _ = wl.make_routing(T, E, tk, seed)
+    ids = ids.clone()
+    if dropped:  # ids == E and > E are both dropped (fused_moe_w4.py:22)
+        ids[0, 0] = E
+        ids[T // 2, tk - 1] = E + 5
+        ids[T - 1, 0] = E
+    hidden = wl.make_hidden(T, 128, seed + 1)
+    sr, off, inv, _ = _route(gpu, ids.to(gpu), hidden.to(gpu), E)
+    ref_sr, _, _, ref_inv = mo.moe_align(ids.numpy(), 1, E)
+    flat = ids.numpy().reshape(-1)
+    counts = np.bincount(flat[flat < E], minlength=E)
+    assert np.array_equal(_np(sr), ref_sr[:T * tk])
+    assert np.array_equal(_np(inv), ref_inv)
+    assert np.array_equal(_np(off), np.concatenate([[0], np.cumsum(counts)]))
+
+
 # ----------------------------------------------------------- expert GEMMs
 def _stage_run(gpu, exp, hidden, ids, act):
     """route -> gate/up -> down through the C ABI; returns GPU tensors."""
