@@ -46,6 +46,8 @@ def _act_code(fn) -> int | None:
     name = (getattr(fn, "__name__", None) or type(fn).__name__) if fn is not None else None
     if name is None:
         return None
+    # as the reference (kernels/fused_moe_w4_v2.py:297): a known tanh-GELU name or
+    # any name containing "gelu" selects the tanh-GELU epilogue
     if name in _TANH_GELU_NAMES or "gelu" in str(name).lower():
         return _lib.ACT_GELU_TANH
     if name in _SILU_NAMES or "silu" in str(name).lower() or "swish" in str(name).lower():

@@ -1,0 +1,77 @@
+"""The C ABI without a GPU: the library loads, exports every entry point that
+include/ksl.h declares (and the ctypes table binds exactly those), and the
+host-side parts (status strings, workspace sizing, argument validation that
+returns before any device work) behave as documented."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tests.conftest import ROOT, load_mod
+
+HEADER = os.path.join(ROOT, "include", "ksl.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(ksl_[a-z0-9_]+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ("ksl_rmsnorm", "ksl_moe_align", "ksl_moe_w4a16_forward", "ksl_moe_layer_forward",
+              "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_version", "ksl_status_string"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = load_mod("_lib")
+    path = lib.LIB_PATH
+    assert os.path.exists(path), "build it first: python knivesysl-diffusion-xe_amd/build.py"
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\s[TW]\s+(ksl_[a-z0-9_]+)$", out, flags=re.M))
+    declared = set(_declared())
+    assert declared <= exported, f"declared but not exported: {sorted(declared - exported)}"
+    assert set(lib.SIGNATURES) == declared, "ctypes table and header disagree"
+
+
+@pytest.fixture(scope="module")
+def L():
+    return load_mod("_lib").load()
+
+
+def test_host_only_calls(L):
+    assert L.ksl_version() >= 1
+    for code, word in ((0, "ok"), (1, "argument"), (2, "shape"), (3, "align")):
+        assert word in L.ksl_status_string(code).decode().lower()
+    assert L.ksl_status_string(99).decode()  # unknown codes still give text
+    a = L.ksl_moe_workspace_bytes(256, 8, 128, 2816, 704)
+    b = L.ksl_moe_workspace_bytes(512, 8, 128, 2816, 704)
+    # sorted rows, offsets, inv, a16, out2, out3 at least
+    assert a >= 256 * 8 * (704 + 2816) * 2 + 256 * 2816 * 2
+    assert b > a
+
+
+def test_validation_returns_before_device_work(L):
+    P = ctypes.c_void_p
+    fake = P(1 << 20)  # never dereferenced: every call below fails its checks first
+    null = P(0)
+    # rows == 0 is a no-op, even with null pointers
+    assert L.ksl_rmsnorm(null, 2, null, 2, null, 2, 0, 128, 128, 128, 1e-6, null) == 0
+    assert L.ksl_rmsnorm(null, 2, null, 2, null, 2, 4, 128, 128, 128, 1e-6, null) == 1     # null x
+    assert L.ksl_rmsnorm(fake, 7, null, 2, fake, 2, 4, 128, 128, 128, 1e-6, null) == 1     # bad dtype
+    # gate/up: null pointers, then H not a multiple of 128, then misalignment
+    assert L.ksl_moe_gateup_act(null, fake, fake, 8, fake, fake, fake, 128, 2816, 704, 1, fake, null) == 1
+    assert L.ksl_moe_gateup_act(fake, fake, fake, 8, fake, fake, fake, 128, 2800, 704, 1, fake, null) == 2
+    assert L.ksl_moe_gateup_act(P((1 << 20) + 8), fake, fake, 8, fake, fake, fake, 128, 2816, 704, 1, fake,
+                                null) == 3
+    # down: I not a multiple of 64, I above 1024
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, fake, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, fake, null) == 2
+    # align: E above the routing limit
+    assert L.ksl_moe_align(fake, 4, 8, 4096, 32, fake, fake, fake, null) == 2

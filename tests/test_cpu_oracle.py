@@ -1,0 +1,311 @@
+"""Pins the oracle (CPU, no GPU): every oracle function is checked against
+something independent of its own formula — hand-computed known answers, the
+stock transformers modules it restates, brute force on tiny inputs, closed
+forms and exact special cases — chosen so that a plausible slip (dropped term,
+swapped nibble, wrong axis, wrong order) fails one of them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as mo
+from oracle import oracle_c
+from tests._helpers import bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
+
+
+def _bf16_row(x: torch.Tensor) -> np.ndarray:
+    return bf16_bits(x.to(torch.bfloat16))
+
+
+# ------------------------------------------------------------------ RMSNorm
+def _stock_rmsnorm(x_bf16: torch.Tensor, w_bf16: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """transformers DiffusionGemmaRMSNorm (TF modeling_diffusion_gemma.py:147-165)."""
+    from transformers.models.diffusion_gemma.modeling_diffusion_gemma import DiffusionGemmaRMSNorm
+    m = DiffusionGemmaRMSNorm(x_bf16.shape[-1], eps=eps, with_scale=w_bf16 is not None)
+    if w_bf16 is not None:
+        with torch.no_grad():
+            m.weight.copy_(w_bf16.float())
+    with torch.no_grad():
+        return m(x_bf16)
+
+
+@pytest.mark.parametrize("with_w", [True, False])
+def test_rmsnorm_matches_stock_module(with_w):
+    g = torch.Generator().manual_seed(5)
+    x = (2 * torch.randn(64, 2816, generator=g)).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(2816, generator=g)).to(torch.bfloat16) if with_w else None
+    ref = bf16_bits(_stock_rmsnorm(x, w, 1e-6))
+    got = mo.rmsnorm(x.float().numpy(), None if w is None else w.float().numpy(), 1e-6)
+    d = ulp_diff16(got, ref)
+    # torch's fp32 mean and pow(-0.5) may round the last fp32 bit differently
+    assert d.max() <= 1
+    assert (d == 0).mean() > 0.99
+
+
+def test_rmsnorm_closed_forms():
+    # constant row c: y = c / sqrt(c^2 + eps) * w -> bf16(w) for eps << c^2
+    w = torch.tensor([0.5, 2.0, -1.0, 3.0] * 32, dtype=torch.bfloat16)
+    x = torch.full((3, 128), 2.0, dtype=torch.bfloat16)
+    got = mo.rmsnorm(x.float().numpy(), w.float().numpy(), 1e-6)
+    assert np.array_equal(got, np.broadcast_to(bf16_bits(w), got.shape))
+    # scale invariance, exact with eps = 0 and a power-of-two factor
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(8, 512, generator=g).to(torch.bfloat16)
+    a = mo.rmsnorm(x.float().numpy(), None, 0.0)
+    b = mo.rmsnorm(4 * x.float().numpy(), None, 0.0)
+    assert np.array_equal(a, b)
+    # w = None and w = 1 agree; the row rms of the output is ~1
+    ones = np.ones(512, dtype=np.float32)
+    assert np.array_equal(mo.rmsnorm(x.float().numpy(), ones, 1e-6), mo.rmsnorm(x.float().numpy(), None, 1e-6))
+    y = mo.bf16_to_f32(a).astype(np.float64)
+    assert np.allclose(np.sqrt((y ** 2).mean(-1)), 1.0, atol=4e-3)
+    # eps enters inside the root: an all-zero row stays zero, a tiny row is damped
+    z = mo.rmsnorm(np.zeros((1, 128), np.float32), None, 1e-6)
+    assert not z.any()
+    t = mo.bf16_to_f32(mo.rmsnorm(np.full((1, 128), 1e-3, np.float32), None, 1e-6))
+    assert np.allclose(t, 1e-3 / np.sqrt(1e-6 + 1e-6), rtol=1e-2)
+
+
+# -------------------------------------------------------- W4 pack / dequant
+def test_quantize_known_answer():
+    # one row, one group of 4: min -1.5, max 3 -> scale 0.3, zero round(1.5/0.3) = 5
+    W = np.array([[0.0, 1.5, 3.0, -1.5]], dtype=np.float32)
+    q, s, z = mo.quantize_w4(W, 4)
+    assert q.tolist() == [[5 | (10 << 4), 15 | (0 << 4)]]  # low nibble = even k
+    assert s.dtype == np.float16 and float(s[0, 0]) == 0.300048828125  # fp16(0.3) = 1229/4096
+    assert float(z[0, 0]) == 5.0
+    Wd = mo.dequant_w4(q, s, z, 4)
+    assert Wd.dtype == np.float16
+    # 5 * 1229/4096 = 1.50024..., 10 * 1229/4096 = 3.00048...: both round to the fp16 grid point
+    assert Wd.tolist() == [[0.0, 1.5, 3.0, -1.5]]
+    # a flat group: the scale clamps at 1e-8/15, zero clamps to 0, q to 15, and the
+    # fp16 scale underflows, so the group dequantises to 0 (the reference's behaviour)
+    q2, s2, z2 = mo.quantize_w4(np.full((1, 4), 2.0, np.float32), 4)
+    assert q2.tolist() == [[0xFF, 0xFF]] and float(z2[0, 0]) == 0.0
+    assert not mo.dequant_w4(q2, s2, z2, 4).any()
+
+
+def test_dequant_is_correctly_rounded_product():
+    g = np.random.default_rng(7)
+    q = g.integers(0, 256, size=(32, 64), dtype=np.uint8)
+    s = g.uniform(0.005, 0.02, size=(32, 2)).astype(np.float16)
+    z = g.integers(0, 16, size=(32, 2)).astype(np.float16)
+    Wd = mo.dequant_w4(q, s, z, 64)
+    nib = np.empty((32, 128), np.int64)
+    nib[:, 0::2] = q & 15
+    nib[:, 1::2] = q >> 4
+    exact = (nib - np.repeat(z.astype(np.float64), 64, 1)) * np.repeat(s.astype(np.float64), 64, 1)
+    assert np.array_equal(Wd, exact.astype(np.float16))  # one rounding of the exact product
+    # unpack is the inverse of the byte packing
+    assert np.array_equal(mo.unpack_nibbles(q).astype(np.int64), nib)
+
+
+def test_quantize_roundtrip_bound():
+    g = np.random.default_rng(8)
+    W = g.standard_normal((16, 256)).astype(np.float32)
+    q, s, z = mo.quantize_w4(W, 128)
+    Wd = mo.dequant_w4(q, s, z, 128).astype(np.float32)
+    step = np.repeat(s.astype(np.float32), 128, 1)
+    assert (np.abs(Wd - W) <= 0.5 * step + 2e-3 * np.abs(W) + 1e-3).all()
+
+
+# ---------------------------------------------------------------- moe_align
+def test_moe_align_known_answer():
+    ids = np.array([[1, 0], [0, 2]])
+    sr, eids, cap, inv = mo.moe_align(ids, 2, 3)
+    assert cap == 10
+    assert sr.tolist() == [1, 2, 0, 4, 3, 4, 4, 4, 4, 4]
+    assert eids.tolist() == [0, 1, 2, 3, 3]
+    assert inv.tolist() == [2, 0, 1, 4]
+
+
+def _align_brute(ids: np.ndarray, bm: int, E: int):
+    flat = np.minimum(ids.reshape(-1), E).tolist()
+    n = len(flat)
+    max_blocks = (n + bm - 1) // bm + E
+    sr = [n] * (max_blocks * bm)
+    eids = [E] * max_blocks
+    inv = [0] * n
+    b = 0
+    for e in range(E):
+        rows = [r for r in range(n) if flat[r] == e]
+        for j, r in enumerate(rows):
+            sr[b * bm + j] = r
+            inv[r] = b * bm + j
+        nb = (len(rows) + bm - 1) // bm
+        for k in range(nb):
+            eids[b + k] = e
+        b += nb
+    return np.array(sr), np.array(eids), max_blocks * bm, np.array(inv)
+
+
+@pytest.mark.parametrize("T,tk,E,bm,seed", [(4, 2, 4, 1, 0), (9, 3, 5, 4, 1), (16, 8, 16, 32, 2), (1, 8, 128, 16, 3),
+                                            (33, 2, 3, 8, 4)])
+def test_moe_align_brute_force_and_c(T, tk, E, bm, seed):
+    g = np.random.default_rng(seed)
+    ids = g.integers(0, E, size=(T, tk))
+    ids[0, 0] = E          # dropped sentinels, == E and > E
+    if T > 1:
+        ids[-1, -1] = E + 3
+    ref = _align_brute(ids, bm, E)
+    got = mo.moe_align(ids, bm, E)
+    assert got[2] == ref[2]
+    for a, b in zip((got[0], got[1], got[3]), (ref[0], ref[1], ref[3])):
+        assert np.array_equal(a, b)
+    cg = oracle_c.moe_align(ids, bm, E)
+    for a, b in zip((cg[0], cg[1], cg[3]), (ref[0], ref[1], ref[3])):
+        assert np.array_equal(a, b)
+
+
+# --------------------------------------------------------------- activations
+@pytest.mark.parametrize("act", [mo.ACT_GELU_TANH, mo.ACT_SILU])
+def test_activation_closed_forms(act):
+    g = np.linspace(-12, 12, 4001).astype(np.float32)
+    got = mo.act_fp32(g, act).astype(np.float64)
+    ref = mo.act_torch_semantics(g.astype(np.float64), act)
+    assert np.allclose(got, ref, rtol=2e-6, atol=2e-6)
+    tref = (torch.nn.functional.gelu(torch.from_numpy(g), approximate="tanh") if act == mo.ACT_GELU_TANH
+            else torch.nn.functional.silu(torch.from_numpy(g))).numpy()
+    assert np.allclose(got, tref, rtol=1e-5, atol=1e-6)
+    assert mo.act_fp32(np.float32([0.0]), act)[0] == 0.0
+
+
+# ---------------------------------------------------------- expert GEMMs
+def _experts(E, H, I, seed):
+    g = np.random.default_rng(seed)
+    gu_q = g.integers(0, 256, size=(E, 2 * I, H // 2), dtype=np.uint8)
+    gu_s = g.uniform(0.005, 0.02, size=(E, 2 * I, H // 128)).astype(np.float16)
+    gu_z = g.integers(0, 16, size=(E, 2 * I, H // 128)).astype(np.float16)
+    dn_q = g.integers(0, 256, size=(E, H, I // 2), dtype=np.uint8)
+    dn_s = g.uniform(0.005, 0.02, size=(E, H, I // 64)).astype(np.float16)
+    dn_z = g.integers(0, 16, size=(E, H, I // 64)).astype(np.float16)
+    return gu_q, gu_s, gu_z, dn_q, dn_s, dn_z
+
+
+def _dequant_torch(q, s, z, gs):
+    """Independent torch form of the W4 dequant: shifts and masks, fp32 product."""
+    qt = torch.from_numpy(q.astype(np.int64))
+    nib = torch.stack((qt & 15, qt >> 4), dim=-1).reshape(*q.shape[:-1], -1).double()
+    zz = torch.from_numpy(z.astype(np.float64)).repeat_interleave(gs, dim=-1)
+    ss = torch.from_numpy(s.astype(np.float64)).repeat_interleave(gs, dim=-1)
+    return ((nib - zz) * ss).half()
+
+
+@pytest.mark.parametrize("act", [mo.ACT_GELU_TANH, mo.ACT_SILU])
+def test_single_expert_reduces_to_dense_linear(act):
+    E, H, I, T = 1, 256, 128, 24
+    gu_q, gu_s, gu_z, dn_q, dn_s, dn_z = _experts(E, H, I, 9)
+    hidden = torch.randn(T, H, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    ids = np.zeros((T, 1), np.int64)
+    w = np.ones((T, 1), np.float32)
+    y = mo.moe_forward(hidden.float().numpy(), gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, ids, w, act)
+    Wgu = _dequant_torch(gu_q[0], gu_s[0], gu_z[0], 128).double()
+    Wdn = _dequant_torch(dn_q[0], dn_s[0], dn_z[0], 64).double()
+    A = hidden.half().double()
+    gu = torch.nn.functional.linear(A, Wgu).float()
+    gate, up = gu[:, :I], gu[:, I:]
+    a = torch.nn.functional.gelu(gate, approximate="tanh") if act == mo.ACT_GELU_TANH else torch.nn.functional.silu(gate)
+    out2 = (a * up).half()
+    out3 = torch.nn.functional.linear(out2.double(), Wdn).float().half()
+    mx, mean = norm_err(y, out3.float().numpy())
+    assert mx < 2e-3 and mean < 2e-4  # fp32 activation rounding may move an fp16 ulp
+
+
+def _moe_brute(hidden_f32, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, ids, w, act):
+    """Per token, per slot, float64 loops from the packed bytes."""
+    T, H = hidden_f32.shape
+    E, twoI, _ = gu_q.shape
+    I = twoI // 2
+    out = np.zeros((T, H), np.float64)
+    for t in range(T):
+        a = hidden_f32[t].astype(np.float16).astype(np.float64)
+        for k in range(ids.shape[1]):
+            e = int(ids[t, k])
+            Wgu = _dequant_torch(gu_q[e], gu_s[e], gu_z[e], 128).double().numpy()
+            Wdn = _dequant_torch(dn_q[e], dn_s[e], dn_z[e], 64).double().numpy()
+            g = (Wgu[:I] @ a).astype(np.float32)
+            u = (Wgu[I:] @ a).astype(np.float32)
+            o2 = (mo.act_torch_semantics(g.astype(np.float64), act) * u).astype(np.float16).astype(np.float64)
+            o3 = (Wdn @ o2).astype(np.float32).astype(np.float16).astype(np.float64)
+            out[t] += float(np.float32(w[t, k])) * o3
+    return out
+
+
+@pytest.mark.parametrize("act", [mo.ACT_GELU_TANH, mo.ACT_SILU])
+def test_moe_forward_brute_force(act):
+    E, H, I, T, tk = 4, 128, 64, 6, 2
+    ex = _experts(E, H, I, 11)
+    g = np.random.default_rng(12)
+    hidden = torch.randn(T, H, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16).float().numpy()
+    ids = np.stack([g.permutation(E)[:tk] for _ in range(T)]).astype(np.int64)
+    w = g.uniform(0.1, 1.0, size=(T, tk)).astype(np.float32)
+    y = mo.moe_forward(hidden, *ex, ids, w, act, block_m=4)
+    ref = _moe_brute(hidden, *ex, ids, w, act)
+    mx, mean = norm_err(y, ref)
+    assert mx < 2e-3 and mean < 2e-4
+    # the compact per-expert form gives the same bits
+    y2, _, _ = mo.moe_forward_per_expert(hidden, *ex, ids, w, act)
+    assert np.array_equal(y, y2)
+
+
+def test_moe_forward_matches_stock_experts_module():
+    """transformers DiffusionGemmaTextExperts.forward on the dequantised
+    weights, the reference's own kill-test comparator (pack_experts.py:142-156:
+    rel_mean < 5e-3, rel_max < 3e-2)."""
+    from transformers.models.diffusion_gemma.configuration_diffusion_gemma import DiffusionGemmaTextConfig
+    from transformers.models.diffusion_gemma.modeling_diffusion_gemma import DiffusionGemmaTextExperts
+    E, H, I, T, tk = 8, 256, 128, 16, 4
+    cfg = DiffusionGemmaTextConfig(num_experts=E, hidden_size=H, moe_intermediate_size=I,
+                                   hidden_activation="gelu_pytorch_tanh")
+    m = DiffusionGemmaTextExperts(cfg)
+    ex = _experts(E, H, I, 14)
+    gu_q, gu_s, gu_z, dn_q, dn_s, dn_z = ex
+    with torch.no_grad():
+        m.gate_up_proj.copy_(torch.stack([_dequant_torch(gu_q[e], gu_s[e], gu_z[e], 128) for e in range(E)]).float())
+        m.down_proj.copy_(torch.stack([_dequant_torch(dn_q[e], dn_s[e], dn_z[e], 64) for e in range(E)]).float())
+    g = torch.Generator().manual_seed(15)
+    hidden = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    p = torch.softmax(torch.randn(T, E, generator=g), -1)
+    w, ids = torch.topk(p, tk, dim=-1)
+    w = w / w.sum(-1, keepdim=True)
+    with torch.no_grad():
+        ref = m(hidden.float(), ids, w).numpy()
+    y = mo.moe_forward(hidden.float().numpy(), *ex, ids.numpy(), w.numpy(), mo.ACT_GELU_TANH)
+    mx, mean = norm_err(y, ref)
+    assert mean < 5e-3 and mx < 3e-2
+
+
+# ------------------------------------------------------------------ combine
+def test_combine_closed_forms_and_c():
+    g = np.random.default_rng(16)
+    T, tk, H = 5, 4, 64
+    out3 = g.standard_normal((T * tk, H)).astype(np.float16)
+    inv = g.permutation(T * tk)
+    # top-1 with weight 1: the identity gather
+    y1 = mo.combine_fma(out3, inv[:T], np.ones((T, 1), np.float32))
+    assert np.array_equal(y1, out3[inv[:T]].astype(np.float32))
+    # equal weights 1/4 over small-integer rows: the exact mean
+    rows = g.integers(-8, 8, size=(T * tk, H)).astype(np.float16)
+    ym = mo.combine_fma(rows, inv, np.full((T, tk), 0.25, np.float32))
+    ref = rows[inv].astype(np.float64).reshape(T, tk, H).mean(1)
+    assert np.array_equal(ym.astype(np.float64), ref)
+    # the C fmaf chain and the numpy emulation agree bit for bit; slot order matters
+    w = g.uniform(0.0, 1.0, size=(T, tk)).astype(np.float32)
+    ybits, yc = oracle_c.combine(out3, inv, w, out_bf16=True)
+    yn = mo.combine_fma(out3, inv, w)
+    assert np.array_equal(yc, yn)
+    assert np.array_equal(ybits, mo.f32_to_bf16(yn))
+    yr = mo.combine_fma(out3, inv.reshape(T, tk)[:, ::-1].reshape(-1), w[:, ::-1].copy())
+    assert not np.array_equal(yr, yn)  # the other order rounds differently somewhere
+
+
+def test_bf16_helpers_round_to_nearest_even():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 65504.0, np.nan], np.float32)
+    b = mo.f32_to_bf16(x)
+    t = bits_to_bf16_tensor(b).float().numpy()
+    assert t[0] == 1.0 and t[1] == 1.0 and t[2] == 1.0 + 2 ** -6 and t[3] == -2.5
+    assert np.isnan(t[5]) and b[5] == 0x7FC0
+    tt = torch.from_numpy(x[:5]).to(torch.bfloat16)
+    assert np.array_equal(b[:5], bf16_bits(tt))
