@@ -72,6 +72,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--skip-kernel-pass", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed region, copy a 512 MiB buffer 5 times (a kernel of known "
+                         "traffic, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -179,6 +182,16 @@ def main() -> int:
         roofline = {"kernel": "gateup_act_kernel", "bound": "hbm", "achieved": round(ach, 1),
                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
                     "traffic": traffic, "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 3)}
+
+    if args.copy_calibration:
+        nbytes = 512 << 20
+        src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 5 copies of {nbytes} bytes")
+        del src, dst
 
     # ---- pass 3: CPU baseline ------------------------------------------------
     cpu = None
