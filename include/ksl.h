@@ -70,7 +70,7 @@ int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, i
 /* Workspace bytes the fused forward needs for these shapes. */
 size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I);
 
-/* The whole W4A16 MoE forward, five launches, no host sync.
+/* The whole W4A16 MoE forward, four launches, no host sync.
  * Replaces fused_moe_w4_v2 (kernels/fused_moe_w4_v2.py:319-371):
  *   align -> gate/up + activation -> down -> fixed-order top-k combine.
  * hidden: [T, H] (bf16/fp16/fp32) with row stride hidden_stride;
