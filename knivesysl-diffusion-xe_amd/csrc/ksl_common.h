@@ -215,13 +215,38 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// ---- RMSNorm of one row, shared by the standalone kernel and the fused layer
-// prep (kernels/fused_rmsnorm.py:10-21). The row is split over LPR = 1 << lpr_log2
-// lanes; lane sl owns 8 consecutive columns per step, NSTEP steps, so
+// ---- RMSNorm arithmetic (kernels/fused_rmsnorm.py:10-21), shared by every
+// kernel that normalises rows so that they all produce the same bits:
+//   ss    = fma chain over the lane's 8-blocks in step order, then a fixed xor
+//           tree over the row's lanes (rms_sumsq8, rms_scale);
+//   r     = 1 / sqrt(ss / cols + eps);
+//   y     = bf16(x * r [* w]), returned as a float (rms_apply).
+template <int XD>
+__device__ __forceinline__ float rms_sumsq8(const Raw8<XD>& v, float ss) {
+    float xf[8];
+    raw_unpack8<XD>(v, xf);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(xf[j], xf[j], ss);
+    return ss;
+}
+__device__ __forceinline__ float rms_scale(float ss, int lpr_log2, int cols, float eps) {
+    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    const float ms = ss / static_cast<float>(cols) + eps;
+    return 1.0f / __builtin_sqrtf(ms);
+}
+template <bool HAS_W>
+__device__ __forceinline__ float rms_apply(float x, float r, float w) {
+    float t = x * r;
+    if constexpr (HAS_W) t = t * w;
+    return bf16_bits_to_f32(f32_to_bf16_bits(t));  // the reference stores bf16
+}
+
+// RMSNorm of one row. The row is split over LPR = 1 << lpr_log2 lanes; lane
+// sl owns 8 consecutive columns per step, NSTEP steps, so
 // c0(s) = s*8*LPR + sl*8. x and w are loaded up front (one round trip, kept
-// as loaded), the fp32 sum of squares is reduced over the LPR lanes by a fixed
-// xor tree, and emit(s, c0, o) receives o[j] = bf16(x * (1/sqrt(ms)) [* w]) as
-// floats for every step with c0 < cols.
+// as loaded), and emit(s, c0, o) receives o[j] = bf16(x * r [* w]) as floats
+// for every step with c0 < cols. Steps past the row end add exact zeros, so
+// any NSTEP that covers the row gives the same bits.
 template <int XD, int WD, int NSTEP, bool HAS_W, typename Emit>
 __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__ xr,
                                         const typename Elem<WD>::T* __restrict__ w, int cols, float eps,
@@ -241,15 +266,8 @@ __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-        float xf[8];
-        raw_unpack8<XD>(xv[s], xf);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(xf[j], xf[j], ss);
-    }
-    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-    const float ms = ss / static_cast<float>(cols) + eps;
-    const float r = 1.0f / __builtin_sqrtf(ms);
+    for (int s = 0; s < NSTEP; ++s) ss = rms_sumsq8<XD>(xv[s], ss);
+    const float r = rms_scale(ss, lpr_log2, cols, eps);
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
         const int c0 = s * stride_cols + sl * 8;
@@ -261,11 +279,7 @@ __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__
         raw_unpack8<XD>(xv[s], xf);
         if constexpr (HAS_W) raw_unpack8<WD>(wv[s], wf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float t = xf[j] * r;
-            if constexpr (HAS_W) t = t * wf[j];
-            o[j] = bf16_bits_to_f32(f32_to_bf16_bits(t));  // the reference stores bf16
-        }
+        for (int j = 0; j < 8; ++j) o[j] = rms_apply<HAS_W>(xf[j], r, HAS_W ? wf[j] : 1.0f);
         emit(s, c0, o);
     }
 }

@@ -17,7 +17,7 @@ int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* 
                int wd, float eps, int64_t H, void* a16, hipStream_t st);
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
-                  int64_t I, int act, void* out2, hipStream_t st);
+                  int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint);
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st);
 
@@ -174,7 +174,7 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     int rc = route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
                            hidden_stride, H, a16, st);
     if (rc) return rc;
-    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st);
+    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
     rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
     if (rc) return rc;
@@ -208,7 +208,7 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
                         norm_w_dtype, eps, H, a16, st);
     if (rc) return rc;
-    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st);
+    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
     rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
     if (rc) return rc;

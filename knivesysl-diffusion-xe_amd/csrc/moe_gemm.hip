@@ -149,6 +149,7 @@ struct GuArgs {
     const f16* gu_z;
     f16* out2;
     int topk, I, H;
+    int early;  // producers issue the first weight groups before reading the routing
 };
 
 template <int NC, int NP, int R>
@@ -165,9 +166,28 @@ struct GuShape {
 // Wave p issues blocks b = p + NP*k (k < KP, b < NB): b < 2*NC is weight block
 // (w, j) = (b/2, b%2) (j: gate, up), else activation block (t, i) =
 // ((b - 2*NC)/4, (b - 2*NC)%4) of M tile t and 32-K step i.
+// Weight blocks of the first groups 0 .. min(R-1, G)-1 of a producer wave (the
+// blocks b = p + NP*k < 2*NC of gateup_produce), issued before the routing is
+// read: they do not depend on it.
+template <int NC, int NP, int R>
+__device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int e, int c0, char* __restrict__ lds) {
+    using S = GuShape<NC, NP, R>;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int p = wave_id() - NC;
+    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int G = A.H >> 7;
+    const int n0 = R - 1 < G ? R - 1 : G;
+    for (int b = p; b < 2 * NC; b += NP) {
+        const int w = b >> 1, j = b & 1;
+        const int64_t row = static_cast<int64_t>(e) * 2 * A.I + (j ? A.I : 0) + c0 + w * 16 + rr;
+        const char* src = reinterpret_cast<const char*>(A.gu_q) + row * (A.H >> 1) + ch * 16;
+        for (int g = 0; g < n0; ++g) dma16(src + g * 64, lds + g * S::kSlot + b * kBlk);
+    }
+}
+
 template <int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
-                                               int m0, int mrows) {
+                                               int m0, int mrows, bool w_issued) {
     using S = GuShape<NC, NP, R>;
     constexpr int NB = 2 * NC + 4 * MT;
     constexpr int KP = (NB + NP - 1) / NP;
@@ -200,11 +220,11 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
         }
         dst[k] = b * kBlk;
     }
-    auto issue = [&](int g, int slot) {
+    auto issue = [&](int g, int slot, bool wts = true) {
         char* base = lds + slot * S::kSlot;
 #pragma unroll
         for (int k = 0; k < KP; ++k)
-            if (k < KP - 1 || full) dma16(src[k] + g * gstep[k], base + dst[k]);
+            if ((k < KP - 1 || full) && (wts || p + NP * k >= 2 * NC)) dma16(src[k] + g * gstep[k], base + dst[k]);
     };
     auto wait_groups = [&](int n) {
         if (full)
@@ -212,10 +232,14 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
         else
             vm_wait_groups<KP - 1, R - 2>(n);
     };
-    // prologue: groups 0 .. R-2
+    // prologue: groups 0 .. R-2 (their weights may be in flight already: then
+    // the activations follow and everything lands before the first barrier)
     int issued = 0;
-    for (; issued < R - 1 && issued < G; ++issued) issue(issued, issued);
-    wait_groups(issued - 1);  // group 0 landed
+    for (; issued < R - 1 && issued < G; ++issued) issue(issued, issued, !w_issued);
+    if (w_issued)
+        vm_wait<0>();
+    else
+        wait_groups(issued - 1);  // group 0 landed
     dma_barrier();
     int slot_next = issued % R;  // slot of group `issued`
     for (int g = 0; g < G; ++g) {
@@ -316,9 +340,13 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
     const int e = tile / nb_per_e;
     const int c0 = (tile - e * nb_per_e) * S::kCols;
+    if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R>(A, e, c0, lds);
     const int start = A.offsets[e];
     const int M = A.offsets[e + 1] - start;
-    if (M <= 0) return;
+    if (M <= 0) {
+        vm_wait<0>();  // early weight loads land before the workgroup's LDS is released
+        return;
+    }
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
     f16* lds_sz = reinterpret_cast<f16*>(lds + R * S::kSlot);
@@ -327,10 +355,11 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     if (wave_id() >= NC) {
         for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
             const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+            const bool w_issued = m0 == 0 && A.early;
             if (mrows <= 16)
-                gateup_produce<NC, NP, R, 1>(A, e, c0, lds, start, m0, mrows);
+                gateup_produce<NC, NP, R, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
             else
-                gateup_produce<NC, NP, R, 2>(A, e, c0, lds, start, m0, mrows);
+                gateup_produce<NC, NP, R, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
         }
     } else {
         // scale / zero table of the workgroup's rows: four [kCols x G] fp16
@@ -888,7 +917,7 @@ int launch_down_dma(const DnArgs& A, unsigned grid, hipStream_t st) {
 
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
-                  int64_t I, int act, void* out2, hipStream_t st) {
+                  int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint) {
     if (!a16 || !sorted_rows || !offsets || !gu_q || !gu_s || !gu_z || !out2) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0 || topk <= 0) return KSL_ERR_SHAPE;
     if (H % 128 != 0 || I % 64 != 0 || H > 128 * kGuMaxG) return KSL_ERR_SHAPE;
@@ -907,6 +936,9 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     A.topk = static_cast<int>(topk);
     A.I = static_cast<int>(I);
     A.H = static_cast<int>(H);
+    // with at least as many routed rows as experts most experts have rows: the
+    // first weight groups go out before the routing is read
+    A.early = nrows_hint >= E ? 1 : 0;
     // widest column block that divides I: 176 (11 consumers), 128, or 64
     // (ring depth 4 where the LDS holds it: 176 columns up to H = 3712)
     if (I % 176 == 0) {
@@ -983,7 +1015,7 @@ extern "C" int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, c
                                   int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                                   int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream) {
     return ksl::launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2,
-                              static_cast<hipStream_t>(stream));
+                              static_cast<hipStream_t>(stream), 0);
 }
 
 extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q,
