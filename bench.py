@@ -169,6 +169,35 @@ def main() -> int:
         if not torch.equal(yf.view(torch.int16), ys.view(torch.int16)):
             log("[bench] WARNING: staged and fused outputs differ")
 
+    # ---- the router (the step before the layer; not part of `value`) --------
+    router_us = None
+    if not args.skip_kernel_pass:
+        g = torch.Generator().manual_seed(7)
+        r_scale = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+        r_proj = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(dev)
+        r_pes = (1 + 0.1 * torch.randn(E, generator=g)).to(torch.bfloat16).to(dev)
+        r_p = torch.empty(T, E, dtype=torch.float32, device=dev)
+        r_w = torch.empty(T, TOPK, dtype=torch.float32, device=dev)
+        r_ids = torch.empty(T, TOPK, dtype=torch.int64, device=dev)
+
+        def route_step():
+            rc = L.ksl_moe_router(p(xg), lib.DTYPE_BF16, H, p(r_scale), p(r_proj), p(r_pes), lib.DTYPE_BF16, 1e-6,
+                                  T, H, E, TOPK, p(r_p), p(r_w), p(r_ids), st)
+            if rc:
+                lib.check(rc, "ksl_moe_router")
+
+        for _ in range(args.warmup):
+            route_step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            route_step()
+        e1.record()
+        torch.cuda.synchronize()
+        router_us = e0.elapsed_time(e1) * 1e3 / args.steps
+        log(f"[bench] router (T={T}, E={E}, top-{TOPK}, not in the layer value): {router_us:.2f} us/launch")
+
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
@@ -234,6 +263,7 @@ def main() -> int:
             "compute": "u4 weights, f16 MFMA operands, f32 accumulate, bf16 in/out",
             "parallelism": "single GPU",
             "kernels_us": {k: round(v["avg_us"], 3) for k, v in kernels.items()},
+            "router_us": None if router_us is None else round(router_us, 3),
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

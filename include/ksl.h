@@ -134,9 +134,11 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
  * out2 fp16 [T*topk, I] row per sorted slot, in the down activation order:
  * the first I128 = I - I % 128 columns in the 128-element group order of a16,
  * a trailing 64-element group (I % 128 == 64) with offset c*16 + i*8 + j
- * stored at i*32 + c*8 + s(j). */
+ * stored at i*32 + c*8 + s(j). T: the tokens of a16 (T*topk routed rows;
+ * with at least E of them the first weight groups are fetched before the
+ * routing is read). */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
-                       int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                       int64_t T, int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
 
 /* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
@@ -151,6 +153,23 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
 int ksl_moe_combine(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
                     int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
                     void* stream);
+
+/* Expert router, the step before the MoE: TF modeling_diffusion_gemma.py:529-548
+ * (DiffusionGemmaTextRouter.forward), its scale-free norm being the fused
+ * RMSNorm as the reference patches every DiffusionGemmaRMSNorm
+ * (kernels/load_w4_checkpoint.py:126-127, kernels/fused_rmsnorm.py:35-48):
+ *   h = bf16(bf16(bf16(rmsnorm(x)) * scale) * fp32(H ** -0.5));
+ *   scores = bf16(h @ proj_w^T); probs = softmax(fp32(scores));
+ *   topk_w, topk_ids = top-k of probs (descending; equal values: lower id),
+ *   topk_w = topk_w / sum(topk_w) * per_expert_scale[topk_ids].
+ * x bf16 or fp16 [T, H] (row stride x_stride elements); scale [H], proj_w
+ * [E, H], per_expert_scale [E] in w_dtype (bf16). probs fp32 [T, E] (the
+ * router probabilities; it also holds the scores between the two launches),
+ * topk_w fp32 [T, topk], topk_ids int64 [T, topk] (the MoE's inputs).
+ * H % 32 == 0, H <= 4096, E % 16 == 0, E <= 256, topk <= min(E, 16). */
+int ksl_moe_router(const void* x, int x_dtype, int64_t x_stride, const void* scale, const void* proj_w,
+                   const void* per_expert_scale, int w_dtype, float eps, int64_t T, int64_t H, int64_t E,
+                   int64_t topk, float* probs, float* topk_w, int64_t* topk_ids, void* stream);
 
 #ifdef __cplusplus
 }

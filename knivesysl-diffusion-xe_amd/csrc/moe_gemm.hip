@@ -1012,10 +1012,10 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
 }  // namespace ksl
 
 extern "C" int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
-                                  int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                                  int64_t T, int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                                   int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream) {
     return ksl::launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2,
-                              static_cast<hipStream_t>(stream), 0);
+                              static_cast<hipStream_t>(stream), T > 0 ? T * topk : 0);
 }
 
 extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q,

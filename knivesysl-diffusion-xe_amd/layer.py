@@ -107,7 +107,7 @@ class LayerRunner:
         _lib.check(rc, "ksl_moe_layer_route")
         if ev:
             ev[1].record()
-        rc = L.ksl_moe_gateup_act(p(self.a16), p(self.sorted_rows), p(self.offsets), tk, p(exp.gu_q),
+        rc = L.ksl_moe_gateup_act(p(self.a16), p(self.sorted_rows), p(self.offsets), T, tk, p(exp.gu_q),
                                   p(exp.gu_s), p(exp.gu_z), E, H, I, exp._ksl_act, p(self.out2), st)
         _lib.check(rc, "ksl_moe_gateup_act")
         if ev:

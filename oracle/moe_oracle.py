@@ -307,6 +307,43 @@ def moe_forward_per_expert(hidden_f32, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
 
 
 # ----------------------------------------------------------------------------
+# Router — TF modeling_diffusion_gemma.py:529-550 (DiffusionGemmaTextRouter.forward),
+# its scale-free norm patched to the fused RMSNorm like every
+# DiffusionGemmaRMSNorm (reference kernels/load_w4_checkpoint.py:126-127,
+# kernels/fused_rmsnorm.py:35-48).
+# ----------------------------------------------------------------------------
+def router(x32: np.ndarray, scale32: np.ndarray, proj32: np.ndarray, pes32: np.ndarray, eps: float, k: int):
+    """Returns (probs fp32 [T,E], top_k_weights fp32 [T,k], top_k_index int64 [T,k]).
+
+    x32: hidden rows as fp32 (bf16 values); scale32 [H], proj32 [E,H],
+    pes32 [E]: the bf16 parameters as fp32.
+      y      = bf16(rmsnorm(x))                      norm, with_scale=False (:530)
+      h1     = bf16(y * scale)                       bf16 * bf16 (:531)
+      h      = bf16(h1 * fp32(H ** -0.5))            bf16 * python scalar (:531)
+      scores = bf16(h @ proj^T), fp32 accumulate     nn.Linear in bf16 (:533)
+      probs  = softmax(fp32(scores))                 (:535)
+      w, idx = top-k of probs, descending            (:538-542); equal values: lower index first
+      w      = w / sum(w) * fp32(per_expert_scale[idx])   (:545, :548)
+    The GEMM accumulates in float64, rounded once to fp32 (any fp32 order
+    approximates that value); softmax likewise in float64, rounded to fp32.
+    """
+    x32 = np.asarray(x32, dtype=np.float32)
+    H = x32.shape[-1]
+    y = bf16_to_f32(rmsnorm(x32, None, eps))
+    h1 = bf16_to_f32(f32_to_bf16((y * np.asarray(scale32, dtype=np.float32)).astype(np.float32)))
+    h = bf16_to_f32(f32_to_bf16((h1 * np.float32(H ** -0.5)).astype(np.float32)))
+    sc = (h.astype(np.float64) @ np.asarray(proj32, dtype=np.float64).T).astype(np.float32)
+    s = bf16_to_f32(f32_to_bf16(sc)).astype(np.float64)
+    e = np.exp(s - s.max(axis=-1, keepdims=True))
+    probs = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    idx = np.argsort(-probs, axis=-1, kind="stable")[:, :k].astype(np.int64)
+    w = np.take_along_axis(probs, idx, axis=-1)
+    w = (w / w.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    w = (w * np.asarray(pes32, dtype=np.float32)[idx]).astype(np.float32)
+    return probs, w, idx
+
+
+# ----------------------------------------------------------------------------
 # Synthetic inputs (the workload definitions) — torch CPU generators so CPU and
 # GPU see identical bits.
 # ----------------------------------------------------------------------------

@@ -64,3 +64,24 @@ def out2_unperm(a: np.ndarray, I: int) -> np.ndarray:
     if i128 == I:
         return act_unperm(a, 128)
     return np.concatenate([act_unperm(a[..., :i128], 128), act_unperm(a[..., i128:], 64)], axis=-1)
+
+
+def assert_topk_equivalent(probs, ids_a, w_a, ids_b, w_b, rtol=1e-5, boundary_rtol=0.0):
+    """Top-k results that may differ only where probabilities tie: per row, the
+    selected probabilities (sorted) agree, every pick of b is a valid top-k
+    member of probs (its probability >= the k-th largest, less boundary_rtol),
+    and ids picked by both carry the same weight. torch.topk itself breaks exact
+    ties in an implementation-defined order."""
+    probs = np.asarray(probs)
+    T, k = ids_a.shape
+    for r in range(T):
+        pa = np.sort(probs[r][ids_a[r]])[::-1]
+        pb = np.sort(probs[r][ids_b[r]])[::-1]
+        np.testing.assert_allclose(pb, pa, rtol=max(rtol, boundary_rtol), err_msg=f"row {r} selected probabilities")
+        kth = np.sort(probs[r])[::-1][k - 1]
+        assert np.all(probs[r][ids_b[r]] >= kth * (1 - boundary_rtol) - 1e-12), f"row {r}: pick below the k-th value"
+        assert len(set(ids_b[r].tolist())) == k, f"row {r}: repeated id"
+        wa = dict(zip(ids_a[r].tolist(), np.asarray(w_a[r]).tolist()))
+        for i, w in zip(ids_b[r].tolist(), np.asarray(w_b[r]).tolist()):
+            if i in wa:
+                assert abs(w - wa[i]) <= rtol * abs(wa[i]) + 1e-9, f"row {r} id {i}: weight {w} vs {wa[i]}"

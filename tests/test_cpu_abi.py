@@ -25,7 +25,8 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ("ksl_rmsnorm", "ksl_moe_align", "ksl_moe_w4a16_forward", "ksl_moe_layer_forward",
-              "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_version", "ksl_status_string"):
+              "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_moe_router", "ksl_version",
+              "ksl_status_string"):
         assert n in names
 
 
@@ -66,12 +67,28 @@ def test_validation_returns_before_device_work(L):
     assert L.ksl_rmsnorm(null, 2, null, 2, null, 2, 4, 128, 128, 128, 1e-6, null) == 1     # null x
     assert L.ksl_rmsnorm(fake, 7, null, 2, fake, 2, 4, 128, 128, 128, 1e-6, null) == 1     # bad dtype
     # gate/up: null pointers, then H not a multiple of 128, then misalignment
-    assert L.ksl_moe_gateup_act(null, fake, fake, 8, fake, fake, fake, 128, 2816, 704, 1, fake, null) == 1
-    assert L.ksl_moe_gateup_act(fake, fake, fake, 8, fake, fake, fake, 128, 2800, 704, 1, fake, null) == 2
-    assert L.ksl_moe_gateup_act(P((1 << 20) + 8), fake, fake, 8, fake, fake, fake, 128, 2816, 704, 1, fake,
+    assert L.ksl_moe_gateup_act(null, fake, fake, 256, 8, fake, fake, fake, 128, 2816, 704, 1, fake, null) == 1
+    assert L.ksl_moe_gateup_act(fake, fake, fake, 256, 8, fake, fake, fake, 128, 2800, 704, 1, fake, null) == 2
+    assert L.ksl_moe_gateup_act(P((1 << 20) + 8), fake, fake, 256, 8, fake, fake, fake, 128, 2816, 704, 1, fake,
                                 null) == 3
     # down: I not a multiple of 64, I above 1024
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, fake, null) == 2
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, fake, null) == 2
     # align: E above the routing limit
     assert L.ksl_moe_align(fake, 4, 8, 4096, 32, fake, fake, fake, null) == 2
+
+
+def test_router_rejects_bad_arguments_without_launching():
+    """Argument checks of ksl_moe_router run on the host (no GPU needed)."""
+    lib = load_mod("_lib")
+    L = lib.load()
+    P = ctypes.c_void_p
+    fake, null = P(1 << 20), P(0)
+    # probs is required (it holds the scores between the two launches)
+    assert L.ksl_moe_router(fake, 2, 2816, fake, fake, fake, 2, 1e-6, 256, 2816, 128, 8, null, fake, fake, null) == 1
+    # E not a multiple of 16, k > 16, H not a multiple of 32
+    assert L.ksl_moe_router(fake, 2, 2816, fake, fake, fake, 2, 1e-6, 256, 2816, 120, 8, fake, fake, fake, null) == 2
+    assert L.ksl_moe_router(fake, 2, 2816, fake, fake, fake, 2, 1e-6, 256, 2816, 128, 17, fake, fake, fake, null) == 2
+    assert L.ksl_moe_router(fake, 2, 2800, fake, fake, fake, 2, 1e-6, 256, 2800, 128, 8, fake, fake, fake, null) == 2
+    # T = 0 is a no-op
+    assert L.ksl_moe_router(null, 2, 2816, null, null, null, 2, 1e-6, 0, 2816, 128, 8, null, null, null, null) == 0

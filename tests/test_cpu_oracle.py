@@ -12,7 +12,7 @@ import torch
 
 from oracle import moe_oracle as mo
 from oracle import oracle_c
-from tests._helpers import bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
+from tests._helpers import assert_topk_equivalent, bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
 
 
 def _bf16_row(x: torch.Tensor) -> np.ndarray:
@@ -309,3 +309,66 @@ def test_bf16_helpers_round_to_nearest_even():
     assert np.isnan(t[5]) and b[5] == 0x7FC0
     tt = torch.from_numpy(x[:5]).to(torch.bfloat16)
     assert np.array_equal(b[:5], bf16_bits(tt))
+
+
+# ------------------------------------------------------------------ router
+def _stock_router(E, H, k, seed):
+    from transformers.models.diffusion_gemma.configuration_diffusion_gemma import DiffusionGemmaTextConfig
+    from transformers.models.diffusion_gemma.modeling_diffusion_gemma import DiffusionGemmaTextRouter
+    cfg = DiffusionGemmaTextConfig(num_experts=E, hidden_size=H, top_k_experts=k, rms_norm_eps=1e-6)
+    m = DiffusionGemmaTextRouter(cfg).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        m.proj.weight.copy_(0.05 * torch.randn(E, H, generator=g))
+        m.scale.copy_(1 + 0.1 * torch.randn(H, generator=g))
+        m.per_expert_scale.copy_(1 + 0.1 * torch.randn(E, generator=g))
+    # the reference patches the router's scale-free norm to the fused RMSNorm
+    # (kernels/load_w4_checkpoint.py:126-127); its output is the oracle's rmsnorm
+    m.norm.forward = lambda hs: torch.from_numpy(mo.bf16_to_f32(mo.rmsnorm(hs.float().numpy(), None, 1e-6))).to(
+        torch.bfloat16)
+    return m
+
+
+def _router_params(m):
+    return (m.scale.detach().float().numpy(), m.proj.weight.detach().float().numpy(),
+            m.per_expert_scale.detach().float().numpy())
+
+
+@pytest.mark.parametrize("T,H,E,k,seed", [(64, 512, 32, 4, 31), (48, 2816, 128, 8, 32)])
+def test_router_matches_stock_module(T, H, E, k, seed):
+    """transformers DiffusionGemmaTextRouter.forward (TF modeling_diffusion_gemma.py:529-548)."""
+    m = _stock_router(E, H, k, seed)
+    x = (2 * torch.randn(T, H, generator=torch.Generator().manual_seed(seed + 100))).to(torch.bfloat16)
+    with torch.no_grad():
+        p, w, i = m(x)
+    po, wo, io = mo.router(x.float().numpy(), *_router_params(m), 1e-6, k)
+    np.testing.assert_allclose(po, p.numpy(), rtol=1e-5, atol=1e-8)
+    # equal bf16 scores give exactly equal probabilities; torch.topk orders such
+    # ties its own way, the oracle takes the lower id first
+    assert_topk_equivalent(po, io, wo, i.numpy(), w.numpy(), rtol=1e-5)
+    assert (io == i.numpy()).all(-1).mean() > 0.5
+
+
+def test_router_closed_forms():
+    T, H, E, k = 5, 256, 16, 4
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(33)).to(torch.bfloat16).float().numpy()
+    ones_h, ones_e = np.ones(H, np.float32), np.ones(E, np.float32)
+    # zero projection: every score 0, probs exactly 1/E; the tie rule takes ids 0..k-1, weights 1/k
+    p, w, i = mo.router(x, ones_h, np.zeros((E, H), np.float32), ones_e, 1e-6, k)
+    assert np.all(p == np.float32(1.0 / E))
+    assert np.array_equal(i, np.broadcast_to(np.arange(k), (T, k)))
+    assert np.allclose(w, 1.0 / k)
+    # k = E with unit expert scales: the weights are the probabilities, summing to 1
+    proj = np.random.default_rng(34).standard_normal((E, H)).astype(np.float32) * 0.05
+    p, w, i = mo.router(x, ones_h, proj, ones_e, 1e-6, E)
+    assert np.allclose(np.take_along_axis(p, i, -1), w, rtol=1e-6)
+    assert np.allclose(w.sum(-1), 1.0, atol=1e-6)
+    assert np.all(np.diff(w, axis=-1) <= 0)
+    # one projection row aligned with a token's normalised row wins for that token,
+    # and the per-expert scale multiplies its weight
+    proj = np.zeros((E, H), np.float32)
+    proj[7] = np.sign(x[2])
+    pes = ones_e.copy()
+    pes[7] = 2.0
+    p, w, i = mo.router(x, ones_h, proj, pes, 1e-6, 1)
+    assert i[2, 0] == 7 and w[2, 0] == 2.0

@@ -146,7 +146,7 @@ def _stage_run(gpu, exp, hidden, ids, act):
     out2 = torch.empty(T * tk, I, dtype=torch.float16, device=gpu)
     out3 = torch.empty(T * tk, H, dtype=torch.float16, device=gpu)
     st = lib.stream_of(hidden)
-    rc = L.ksl_moe_gateup_act(lib.ptr(a16), lib.ptr(sr), lib.ptr(off), tk, lib.ptr(exp.gu_q), lib.ptr(exp.gu_s),
+    rc = L.ksl_moe_gateup_act(lib.ptr(a16), lib.ptr(sr), lib.ptr(off), T, tk, lib.ptr(exp.gu_q), lib.ptr(exp.gu_s),
                               lib.ptr(exp.gu_z), E, H, I, act, lib.ptr(out2), st)
     lib.check(rc, "ksl_moe_gateup_act")
     rc = L.ksl_moe_down(lib.ptr(out2), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
