@@ -180,23 +180,42 @@ def main() -> int:
         r_w = torch.empty(T, TOPK, dtype=torch.float32, device=dev)
         r_ids = torch.empty(T, TOPK, dtype=torch.int64, device=dev)
 
-        def route_step():
+        def route_step(stream):
             rc = L.ksl_moe_router(p(xg), lib.DTYPE_BF16, H, p(r_scale), p(r_proj), p(r_pes), lib.DTYPE_BF16, 1e-6,
-                                  T, H, E, TOPK, p(r_p), p(r_w), p(r_ids), st)
+                                  T, H, E, TOPK, p(r_p), p(r_w), p(r_ids), stream)
             if rc:
                 lib.check(rc, "ksl_moe_router")
 
         for _ in range(args.warmup):
-            route_step()
+            route_step(st)
         torch.cuda.synchronize()
+        ref_w, ref_ids = r_w.clone(), r_ids.clone()
+        # a few microseconds of GPU work per call: launched one by one from Python
+        # the host is the bottleneck, so the calls are captured in a graph and
+        # replayed (no memset nodes: the router writes every output)
+        n_cap = 20
+        cap_stream = torch.cuda.Stream()
+        cap_stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap_stream):
+            cap = lib.stream_of(xg)  # the capturing stream
+            for _ in range(n_cap):
+                route_step(cap)
+        torch.cuda.current_stream().wait_stream(cap_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        if not (torch.equal(r_w, ref_w) and torch.equal(r_ids, ref_ids)):
+            log("[bench] WARNING: router graph replay differs from the eager call")
+        reps = max(1, args.steps // n_cap)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(args.steps):
-            route_step()
+        for _ in range(reps):
+            graph.replay()
         e1.record()
         torch.cuda.synchronize()
-        router_us = e0.elapsed_time(e1) * 1e3 / args.steps
-        log(f"[bench] router (T={T}, E={E}, top-{TOPK}, not in the layer value): {router_us:.2f} us/launch")
+        router_us = e0.elapsed_time(e1) * 1e3 / (reps * n_cap)
+        log(f"[bench] router (T={T}, E={E}, top-{TOPK}, not in the layer value): {router_us:.2f} us/call "
+            f"(graph replay of {n_cap} calls)")
 
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None

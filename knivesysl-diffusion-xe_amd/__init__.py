@@ -6,6 +6,7 @@ Drop-in modules, named after the reference's kernel modules:
   fused_moe_w4_v2  fused_moe_w4_v2 (W4A16 128-expert fused MoE forward)
   pack_experts     fused_experts_forward, GU_GS, DN_GS
   layer            moe_layer: RMSNorm followed by the MoE forward
+  router           router_forward, patch_routers (the expert router, the step before)
 All compute runs in libksl.so (hand-written HIP, C ABI in include/ksl.h).
 """
 from . import _lib
@@ -13,5 +14,7 @@ from .fused_moe_w4 import moe_align
 from .fused_moe_w4_v2 import fused_moe_w4_v2
 from .fused_rmsnorm import fused_rmsnorm, patch_rmsnorms
 from .pack_experts import fused_experts_forward
+from .router import patch_routers, router_forward
 
-__all__ = ["fused_rmsnorm", "patch_rmsnorms", "moe_align", "fused_moe_w4_v2", "fused_experts_forward"]
+__all__ = ["fused_rmsnorm", "patch_rmsnorms", "moe_align", "fused_moe_w4_v2", "fused_experts_forward",
+           "router_forward", "patch_routers"]
