@@ -217,6 +217,96 @@ def main() -> int:
         log(f"[bench] router (T={T}, E={E}, top-{TOPK}, not in the layer value): {router_us:.2f} us/call "
             f"(graph replay of {n_cap} calls)")
 
+    # ---- the block's tail (the step after the layer; not part of `value`) ---
+    # TF modeling_diffusion_gemma.py:733-743 after the experts: post norm 2,
+    # + hidden_states_1, post norm, + residual, * layer_scalar. Fused: one
+    # combine launch with the tail in its epilogue. Unfused, as the reference
+    # runs it: the combine, then fused_rmsnorm, add, fused_rmsnorm, add, mul.
+    tail = None
+    if not args.skip_kernel_pass:
+        frm = importlib.import_module(f"{PKG}.fused_rmsnorm")
+        g = torch.Generator().manual_seed(8)
+        t_h1 = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        t_w2 = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+        t_wp = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+        t_ls = torch.tensor([0.75], dtype=torch.bfloat16, device=dev)
+        t_y = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        t_m = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        b_y = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        r_p = torch.empty(T, E, dtype=torch.float32, device=dev)
+        b_w = torch.empty(T, TOPK, dtype=torch.float32, device=dev)
+        b_ids = torch.empty(T, TOPK, dtype=torch.int64, device=dev)
+        g = torch.Generator().manual_seed(7)
+        r_scale = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+        r_proj = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(dev)
+        r_pes = (1 + 0.1 * torch.randn(E, generator=g)).to(torch.bfloat16).to(dev)
+        exp0 = sets[0]
+        unfused_out = []
+
+        def tail_fused(stream):
+            rc = L.ksl_moe_combine_post(p(runner.out3), p(runner.inv), p(wg), lib.DTYPE_F32, T, TOPK, H,
+                                        p(t_h1), H, p(xg), H, p(t_w2), 1e-6, p(t_wp), 1e-6, p(t_ls), lib.DTYPE_BF16,
+                                        p(t_y), H, stream)
+            if rc:
+                lib.check(rc, "ksl_moe_combine_post")
+
+        def tail_unfused(stream):
+            rc = L.ksl_moe_combine(p(runner.out3), p(runner.inv), p(wg), lib.DTYPE_F32, T, TOPK, H, p(t_m),
+                                   lib.DTYPE_BF16, H, stream)
+            if rc:
+                lib.check(rc, "ksl_moe_combine")
+            o = xg + frm.fused_rmsnorm(t_h1 + frm.fused_rmsnorm(t_m, t_w2, 1e-6), t_wp, 1e-6)
+            o *= t_ls
+            unfused_out.append(o)
+
+        def block(stream):
+            # the layer's whole MoE branch: router, then norm + experts + tail
+            rc = L.ksl_moe_router(p(xg), lib.DTYPE_BF16, H, p(r_scale), p(r_proj), p(r_pes), lib.DTYPE_BF16, 1e-6,
+                                  T, H, E, TOPK, p(r_p), p(b_w), p(b_ids), stream)
+            if rc:
+                lib.check(rc, "ksl_moe_router")
+            rc = L.ksl_moe_block_forward(p(xg), H, p(nwg), 1e-6, p(b_ids), p(b_w), lib.DTYPE_F32,
+                                         p(exp0.gu_q), p(exp0.gu_s), p(exp0.gu_z), p(exp0.dn_q), p(exp0.dn_s),
+                                         p(exp0.dn_z), T, TOPK, E, H, I, exp0._ksl_act, p(t_h1), H, p(t_w2), 1e-6,
+                                         p(t_wp), 1e-6, p(t_ls), lib.DTYPE_BF16, p(b_y), H, p(ws), ws.numel(),
+                                         stream)
+            if rc:
+                lib.check(rc, "ksl_moe_block_forward")
+
+        def graph_us(fn, n_cap):
+            for _ in range(3):
+                fn(st)
+            torch.cuda.synchronize()
+            cap_stream = torch.cuda.Stream()
+            cap_stream.wait_stream(torch.cuda.current_stream())
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=cap_stream):
+                cap = lib.stream_of(xg)
+                for _ in range(n_cap):
+                    fn(cap)
+            torch.cuda.current_stream().wait_stream(cap_stream)
+            gr.replay()
+            torch.cuda.synchronize()
+            reps = max(1, args.steps // n_cap)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                gr.replay()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / (reps * n_cap)
+
+        fused_us = graph_us(tail_fused, 20)
+        fused_y = t_y.clone()
+        unfused_us = graph_us(tail_unfused, 20)
+        ndiff = int((unfused_out[-1].view(torch.int16) != fused_y.view(torch.int16)).sum().item())
+        block_us = graph_us(block, 5)
+        tail = {"fused_us": round(fused_us, 3), "unfused_us": round(unfused_us, 3), "block_us": round(block_us, 3),
+                "fused_vs_unfused_differing_elements": ndiff}
+        log(f"[bench] block tail (not in the layer value): fused into the combine {fused_us:.2f} us, "
+            f"combine + 5 separate calls {unfused_us:.2f} us ({ndiff} of {T * H} elements differ by the "
+            f"row-sum order); router + block forward {block_us:.2f} us (graph replay)")
+
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
@@ -283,6 +373,7 @@ def main() -> int:
             "parallelism": "single GPU",
             "kernels_us": {k: round(v["avg_us"], 3) for k, v in kernels.items()},
             "router_us": None if router_us is None else round(router_us, 3),
+            "block_tail": tail,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -171,6 +171,43 @@ int ksl_moe_router(const void* x, int x_dtype, int64_t x_stride, const void* sca
                    const void* per_expert_scale, int w_dtype, float eps, int64_t T, int64_t H, int64_t E,
                    int64_t topk, float* probs, float* topk_w, int64_t* topk_ids, void* stream);
 
+/* The combine fused with the feed-forward block's tail, the step after the
+ * MoE: TF modeling_diffusion_gemma.py:734-744 (decoder and encoder layers),
+ * every RMSNorm being the fused RMSNorm (kernels/fused_rmsnorm.py:10-21):
+ *   m  = bf16(combine as ksl_moe_combine)
+ *   s  = bf16(h1 + bf16(m * r(m) * post2_w))           post_feedforward_layernorm_2, + hidden_states_1
+ *   o  = bf16(residual + bf16(s * r(s) * post_w))     post_feedforward_layernorm, + residual
+ *   y  = bf16(o * layer_scalar)                        hidden_states *= layer_scalar
+ * r(v) = 1 / sqrt(sum(v^2) / H + eps) with post2_eps resp. post_eps. One
+ * launch, one workgroup per token. h1, residual, post2_w, post_w, y: bf16
+ * (the layer's dtype); layer_scalar: one fp32 or bf16 element (ls_dtype), or
+ * NULL for 1. H % 8 == 0, H <= 8192. y may be the residual or h1 buffer
+ * (same stride): each element is read before it is written, by one thread.
+ * Not a reference entry point: the reference runs the tail as five torch
+ * calls after _combine (kernels/fused_moe_w4_v2.py:371). */
+int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                         int64_t T, int64_t topk, int64_t H, const void* h1, int64_t h1_stride,
+                         const void* residual, int64_t residual_stride, const void* post2_w,
+                         float post2_eps, const void* post_w, float post_eps, const void* layer_scalar,
+                         int ls_dtype, void* y, int64_t y_stride, void* stream);
+
+/* The decoder layer's MoE branch and tail, four launches (TF
+ * modeling_diffusion_gemma.py:729-744 after the router): x is the residual
+ * (hidden_states_flat), bf16 [T, H];
+ *   moe = experts(rmsnorm(x) * pre_norm_w, topk_ids, topk_w)   as ksl_moe_layer_forward
+ *   y   = the tail of ksl_moe_combine_post with residual = x.
+ * Same workspace as ksl_moe_w4a16_forward; same contracts as
+ * ksl_moe_layer_forward (H <= 4096) and ksl_moe_combine_post. Not a
+ * reference entry point (see ksl_moe_combine_post). */
+int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
+                          const int64_t* topk_ids, const void* topk_w, int w_dtype,
+                          const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
+                          int64_t topk, int64_t E, int64_t H, int64_t I, int act, const void* h1,
+                          int64_t h1_stride, const void* post2_w, float post2_eps, const void* post_w,
+                          float post_eps, const void* layer_scalar, int ls_dtype, void* y,
+                          int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,8 @@ Drop-in modules, named after the reference's kernel modules:
   pack_experts     fused_experts_forward, GU_GS, DN_GS
   layer            moe_layer: RMSNorm followed by the MoE forward
   router           router_forward, patch_routers (the expert router, the step before)
+  moe_block        moe_block_forward, layer_forward, patch_moe_blocks (the MoE branch
+                   with the layer's tail fused into the combine, the step after)
 All compute runs in libksl.so (hand-written HIP, C ABI in include/ksl.h).
 """
 from . import _lib
@@ -14,7 +16,8 @@ from .fused_moe_w4 import moe_align
 from .fused_moe_w4_v2 import fused_moe_w4_v2
 from .fused_rmsnorm import fused_rmsnorm, patch_rmsnorms
 from .pack_experts import fused_experts_forward
+from .moe_block import layer_forward, moe_block_forward, patch_moe_blocks
 from .router import patch_routers, router_forward
 
 __all__ = ["fused_rmsnorm", "patch_rmsnorms", "moe_align", "fused_moe_w4_v2", "fused_experts_forward",
-           "router_forward", "patch_routers"]
+           "router_forward", "patch_routers", "moe_block_forward", "layer_forward", "patch_moe_blocks"]

@@ -45,6 +45,11 @@ SIGNATURES = {
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P], _I),
     "ksl_moe_router": ([_P, _I, _I64, _P, _P, _P, _I, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
+    "ksl_moe_combine_post": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _P, _F,
+                              _P, _I, _P, _I64, _P], _I),
+    "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P,
+                               _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _F, _P, _F, _P, _I,
+                               _P, _I64, _P, _SZ, _P], _I),
 }
 
 _lock = threading.Lock()

@@ -32,6 +32,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// fp32 rounded to the nearest bf16 value (as a float).
+__device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// Wave-wide reductions of the ROCm device library (declared in the HIP
+// headers, amd_warp_sync_functions.h): fixed DPP trees, deterministic; every
+// lane of the wave receives the result.
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
+extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+
 __device__ __forceinline__ uint16_t f16_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 
 // Element access by storage dtype code.
@@ -219,7 +229,7 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 // kernel that normalises rows so that they all produce the same bits:
 //   ss    = fma chain over the lane's 8-blocks in step order, then a fixed xor
 //           tree over the row's lanes (rms_sumsq8, rms_scale);
-//   r     = 1 / sqrt(ss / cols + eps);
+//   r     = 1 / sqrt(ss / cols + eps)                      (rms_inv);
 //   y     = bf16(x * r [* w]), returned as a float (rms_apply).
 template <int XD>
 __device__ __forceinline__ float rms_sumsq8(const Raw8<XD>& v, float ss) {
@@ -229,10 +239,13 @@ __device__ __forceinline__ float rms_sumsq8(const Raw8<XD>& v, float ss) {
     for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(xf[j], xf[j], ss);
     return ss;
 }
-__device__ __forceinline__ float rms_scale(float ss, int lpr_log2, int cols, float eps) {
-    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+__device__ __forceinline__ float rms_inv(float ss, int cols, float eps) {
     const float ms = ss / static_cast<float>(cols) + eps;
     return 1.0f / __builtin_sqrtf(ms);
+}
+__device__ __forceinline__ float rms_scale(float ss, int lpr_log2, int cols, float eps) {
+    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    return rms_inv(ss, cols, eps);
 }
 template <bool HAS_W>
 __device__ __forceinline__ float rms_apply(float x, float r, float w) {

@@ -25,26 +25,15 @@ namespace {
 
 constexpr int kCombThreads = 256;
 
-template <int WD, int YD>
-__global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __restrict__ out3,
-                                                              const int32_t* __restrict__ inv,
-                                                              const void* __restrict__ wv, int64_t T,
-                                                              int topk, int64_t H, void* __restrict__ yv,
-                                                              int64_t ys) {
-    typedef typename Elem<WD>::T WT;
-    typedef typename Elem<YD>::T YT;
-    const WT* w = static_cast<const WT*>(wv);
-    YT* y = static_cast<YT*>(yv);
-    const int64_t hv = H / 8;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kCombThreads + threadIdx.x;
-    const int64_t t = idx / hv;
-    if (t >= T) return;
-    const int64_t c0 = (idx - t * hv) * 8;
-    float acc[8];
+// acc[j] = sum over slots k in order of fp32(w[t,k]) * fp32(out3[inv[t*topk+k], c0+j]).
+// 8 slots at a time: all index/weight loads (uniform per token), then all row
+// loads (clamped slot index: one round trip each), then the FMA chain in slot order.
+template <int WD>
+__device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const int32_t* __restrict__ inv,
+                                            const typename Elem<WD>::T* __restrict__ w, int64_t t, int topk,
+                                            int64_t H, int64_t c0, float (&acc)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    // 8 slots at a time: all index/weight loads, then all row loads (clamped slot
-    // index: one round trip each), then the FMA chain in slot order.
     for (int k0 = 0; k0 < topk; k0 += 8) {
         int32_t r[8];
         float wk[8];
@@ -65,6 +54,23 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
             }
         }
     }
+}
+
+template <int WD, int YD>
+__global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __restrict__ out3,
+                                                              const int32_t* __restrict__ inv,
+                                                              const void* __restrict__ wv, int64_t T,
+                                                              int topk, int64_t H, void* __restrict__ yv,
+                                                              int64_t ys) {
+    typedef typename Elem<YD>::T YT;
+    YT* y = static_cast<YT*>(yv);
+    const int64_t hv = H / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kCombThreads + threadIdx.x;
+    const int64_t t = idx / hv;
+    if (t >= T) return;
+    const int64_t c0 = (idx - t * hv) * 8;
+    float acc[8];
+    combine_acc<WD>(out3, inv, static_cast<const typename Elem<WD>::T*>(wv), t, topk, H, c0, acc);
     store8<YD>(y + t * ys + c0, acc);
 }
 
@@ -94,6 +100,98 @@ int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w
     return KSL_OK;
 }
 
+// ---- combine + the feed-forward block's tail --------------------------------
+// After the experts the decoder layer computes (TF modeling_diffusion_gemma.py:734-744,
+// every RMSNorm being the fused RMSNorm of kernels/fused_rmsnorm.py:10-21):
+//   m  = bf16(combine)                    experts' output, hidden dtype bf16
+//   n2 = bf16(m * r(m) * w2)              post_feedforward_layernorm_2
+//   s  = bf16(h1 + n2)                    hidden_states_1 + hidden_states_2
+//   n  = bf16(s * r(s) * w)               post_feedforward_layernorm
+//   o  = bf16(res + n)                    residual + hidden_states
+//   y  = bf16(o * layer_scalar)           hidden_states *= layer_scalar
+// with r(v) = 1 / sqrt(sum(v^2) / H + eps). One workgroup per token, thread i
+// owning columns 8i..8i+7 (threads past the row end hold zeros). A row sum is
+// a per-thread FMA chain, a DPP wave reduction and the wave partials added in
+// wave order: the same bits every run.
+constexpr int kPostMaxWaves = 16;
+constexpr int kPostMaxH = kPostMaxWaves * kWave * 8;
+
+struct PostArgs {
+    const f16* out3;
+    const int32_t* inv;
+    const void* w;          // top-k weights, dtype WD
+    const uint16_t* h1;     // bf16 [T, h1s]
+    const uint16_t* res;    // bf16 [T, rs]
+    const uint16_t* w2;     // bf16 [H]: post_feedforward_layernorm_2 weight
+    const uint16_t* wp;     // bf16 [H]: post_feedforward_layernorm weight
+    const void* ls;         // layer scalar (one element) or null for 1
+    uint16_t* y;            // bf16 [T, ys]
+    int64_t h1s, rs, ys;
+    float eps2, eps;
+    int topk, H, ls_dt;
+};
+
+__device__ __forceinline__ float block_row_sum(float v, float* part, int nwaves) {
+    v = __ockl_wfred_add_f32(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nwaves; ++i) s += part[i];
+    return s;
+}
+
+template <int WD>
+__global__ __launch_bounds__(kPostMaxWaves * kWave) void combine_post_kernel(PostArgs A) {
+    constexpr int BF = KSL_DTYPE_BF16;
+    __shared__ float part[2][kPostMaxWaves];
+    const int64_t t = blockIdx.x;
+    const int nw = static_cast<int>(blockDim.x) / kWave;
+    const int64_t c0 = static_cast<int64_t>(threadIdx.x) * 8;
+    const bool ok = c0 < A.H;
+    // the token's other operands are independent of the gather: issue them first
+    Raw8<BF> hv{}, rv{}, w2v{}, wpv{};
+    if (ok) {
+        hv = raw_load8<BF>(A.h1 + t * A.h1s + c0);
+        rv = raw_load8<BF>(A.res + t * A.rs + c0);
+        w2v = raw_load8<BF>(A.w2 + c0);
+        wpv = raw_load8<BF>(A.wp + c0);
+    }
+    float ls = 1.0f;
+    if (A.ls)
+        ls = A.ls_dt == KSL_DTYPE_F32 ? *static_cast<const float*>(A.ls)
+                                      : bf16_bits_to_f32(*static_cast<const uint16_t*>(A.ls));
+    float m[8];
+    if (ok) {
+        combine_acc<WD>(A.out3, A.inv, static_cast<const typename Elem<WD>::T*>(A.w), t, A.topk, A.H, c0, m);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m[j] = 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        m[j] = bf16r(m[j]);
+        ss = __builtin_fmaf(m[j], m[j], ss);
+    }
+    const float r2 = rms_inv(block_row_sum(ss, part[0], nw), A.H, A.eps2);
+    float hf[8], w2f[8], s[8];
+    raw_unpack8<BF>(hv, hf);
+    raw_unpack8<BF>(w2v, w2f);
+    ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        s[j] = bf16r(hf[j] + rms_apply<true>(m[j], r2, w2f[j]));
+        ss = __builtin_fmaf(s[j], s[j], ss);
+    }
+    const float r = rms_inv(block_row_sum(ss, part[1], nw), A.H, A.eps);
+    float rf[8], wpf[8], o[8];
+    raw_unpack8<BF>(rv, rf);
+    raw_unpack8<BF>(wpv, wpf);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = bf16r(bf16r(rf[j] + rms_apply<true>(s[j], r, wpf[j])) * ls);
+    if (ok) store8<BF>(A.y + t * A.ys + c0, o);
+}
+
 }  // namespace
 
 int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
@@ -109,6 +207,60 @@ int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, 
         case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16>(yd, out3, inv, w, T, topk, H, y, ys, st);
     }
     return KSL_ERR_ARG;
+}
+
+// Argument checks of the tail (everything but the experts' rows), made before
+// any launch of a fused forward.
+static int check_post(int64_t T, int64_t topk, int64_t H, int wd, const void* h1, int64_t h1s,
+                      const void* res, int64_t rs, const void* w2, const void* wp, const void* ls, int ls_dt,
+                      const void* y, int64_t ys) {
+    if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0 || H > kPostMaxH) return KSL_ERR_SHAPE;
+    if (T == 0) return KSL_OK;
+    if (!h1 || !res || !w2 || !wp || !y) return KSL_ERR_ARG;
+    if (ls && ls_dt != KSL_DTYPE_F32 && ls_dt != KSL_DTYPE_BF16) return KSL_ERR_ARG;
+    if (wd != KSL_DTYPE_F32 && wd != KSL_DTYPE_F16 && wd != KSL_DTYPE_BF16) return KSL_ERR_ARG;
+    if (h1s < H || rs < H || ys < H) return KSL_ERR_SHAPE;
+    if (h1s % 8 || rs % 8 || ys % 8) return KSL_ERR_ALIGN;
+    for (const void* p : {h1, res, w2, wp, y})
+        if (reinterpret_cast<uintptr_t>(p) % 16) return KSL_ERR_ALIGN;
+    return KSL_OK;
+}
+
+int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
+                        int64_t topk, int64_t H, const void* h1, int64_t h1s, const void* res, int64_t rs,
+                        const void* w2, float eps2, const void* wp, float eps, const void* ls, int ls_dt,
+                        void* y, int64_t ys, hipStream_t st) {
+    const int rc = check_post(T, topk, H, wd, h1, h1s, res, rs, w2, wp, ls, ls_dt, y, ys);
+    if (rc || T == 0) return rc;
+    if (!out3 || !inv || !w) return KSL_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(out3) % 16) return KSL_ERR_ALIGN;
+    PostArgs A;
+    A.out3 = static_cast<const f16*>(out3);
+    A.inv = inv;
+    A.w = w;
+    A.h1 = static_cast<const uint16_t*>(h1);
+    A.res = static_cast<const uint16_t*>(res);
+    A.w2 = static_cast<const uint16_t*>(w2);
+    A.wp = static_cast<const uint16_t*>(wp);
+    A.ls = ls;
+    A.y = static_cast<uint16_t*>(y);
+    A.h1s = h1s;
+    A.rs = rs;
+    A.ys = ys;
+    A.eps2 = eps2;
+    A.eps = eps;
+    A.topk = static_cast<int>(topk);
+    A.H = static_cast<int>(H);
+    A.ls_dt = ls_dt;
+    const int threads = static_cast<int>((H / 8 + kWave - 1) / kWave) * kWave;
+    const dim3 grid(static_cast<unsigned>(T)), block(threads);
+    switch (wd) {
+        case KSL_DTYPE_F32: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_F32>, grid, block, 0, st, A); break;
+        case KSL_DTYPE_F16: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_F16>, grid, block, 0, st, A); break;
+        default: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_BF16>, grid, block, 0, st, A); break;
+    }
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }
 
 // Workspace layout of the fused forward (each region 256-byte aligned):
@@ -141,6 +293,17 @@ extern "C" int ksl_moe_combine(const void* out3, const int32_t* inv, const void*
                                int64_t y_stride, void* stream) {
     return ksl::launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride,
                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                                    int64_t T, int64_t topk, int64_t H, const void* h1, int64_t h1_stride,
+                                    const void* residual, int64_t residual_stride, const void* post2_w,
+                                    float post2_eps, const void* post_w, float post_eps,
+                                    const void* layer_scalar, int ls_dtype, void* y, int64_t y_stride,
+                                    void* stream) {
+    return ksl::launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, residual,
+                                    residual_stride, post2_w, post2_eps, post_w, post_eps, layer_scalar,
+                                    ls_dtype, y, y_stride, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
@@ -213,6 +376,44 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+}
+
+extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
+                                     const int64_t* topk_ids, const void* topk_w, int w_dtype,
+                                     const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
+                                     int64_t topk, int64_t E, int64_t H, int64_t I, int act, const void* h1,
+                                     int64_t h1_stride, const void* post2_w, float post2_eps,
+                                     const void* post_w, float post_eps, const void* layer_scalar,
+                                     int ls_dtype, void* y, int64_t y_stride, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
+    if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    int rc = check_post(T, topk, H, w_dtype, h1, h1_stride, x, x_stride, post2_w, post_w, layer_scalar,
+                        ls_dtype, y, y_stride);
+    if (rc || T == 0) return rc;
+    const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
+    if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return KSL_ERR_ALIGN;
+    char* ws = static_cast<char*>(workspace);
+    int32_t* sorted_rows = reinterpret_cast<int32_t*>(ws + L.sorted_rows);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    int32_t* inv = reinterpret_cast<int32_t*>(ws + L.inv);
+    void* a16 = ws + L.a16;
+    void* out2 = ws + L.out2;
+    void* out3 = ws + L.out3;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, KSL_DTYPE_BF16, x_stride, pre_norm_w,
+                    KSL_DTYPE_BF16, pre_eps, H, a16, st);
+    if (rc) return rc;
+    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
+    if (rc) return rc;
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    if (rc) return rc;
+    return launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, x, x_stride, post2_w,
+                               post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);
 }
 
 extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,

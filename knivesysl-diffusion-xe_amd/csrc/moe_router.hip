@@ -45,8 +45,6 @@ struct RouterArgs {
     int T, H, E, k;
 };
 
-__device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
-
 // bf16 rounding (round to nearest even) by the gfx950 conversion instruction:
 // the same value as bf16r for every non-NaN input (fp32 denormals are kept,
 // .amdhsa_float_denorm_mode_32 = 3); a NaN stays a NaN. Used for the router's
@@ -157,12 +155,6 @@ __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A)
         if (t < A.T) A.probs[static_cast<int64_t>(t) * E + tile * 16 + (l & 15)] = bf16r(sum);
     }
 }
-
-// Wave-wide reductions of the ROCm device library (declared in the HIP
-// headers, amd_warp_sync_functions.h): fixed DPP trees, deterministic.
-extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
-extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
-extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
 
 // One wave per token: softmax over the scores in probs (in place), then k
 // rounds of a wave arg-max on 64-bit keys (probability bits, then the inverted

@@ -344,6 +344,34 @@ def router(x32: np.ndarray, scale32: np.ndarray, proj32: np.ndarray, pes32: np.n
 
 
 # ----------------------------------------------------------------------------
+# Feed-forward block tail, the step after the MoE — TF
+# modeling_diffusion_gemma.py:733-743 (DiffusionGemmaDecoderTextLayer.forward;
+# DiffusionGemmaEncoderTextLayer.forward :655-665 is the same), its RMSNorms
+# patched to the fused RMSNorm (kernels/load_w4_checkpoint.py:126-127).
+# ----------------------------------------------------------------------------
+def block_tail(m_bits: np.ndarray, h1_32: np.ndarray, res32: np.ndarray, post2_w32: np.ndarray,
+               post_w32: np.ndarray, ls: float, eps2: float, eps: float) -> np.ndarray:
+    """Returns the layer output as bf16 bits [T, H].
+
+    m_bits: the experts' output as bf16 bits (fused_moe_w4_v2 returns the
+    hidden dtype, kernels/fused_moe_w4_v2.py:260-263); h1_32, res32: the bf16
+    hidden_states_1 and residual as fp32; post2_w32, post_w32: the bf16 norm
+    weights as fp32; ls: the layer scalar's value.
+      n2 = rmsnorm(m, post2_w)       post_feedforward_layernorm_2 (:735)
+      s  = bf16(h1 + n2)             bf16 + bf16, fp32 sum (:738)
+      n  = rmsnorm(s, post_w)        post_feedforward_layernorm (:740)
+      o  = bf16(res + n)             (:741)
+      y  = bf16(o * ls)              hidden_states *= layer_scalar, fp32 product (:743)
+    """
+    m32 = bf16_to_f32(m_bits)
+    n2 = bf16_to_f32(rmsnorm(m32, post2_w32, eps2))
+    s = bf16_to_f32(f32_to_bf16((np.asarray(h1_32, dtype=np.float32) + n2).astype(np.float32)))
+    n = bf16_to_f32(rmsnorm(s, post_w32, eps))
+    o = bf16_to_f32(f32_to_bf16((np.asarray(res32, dtype=np.float32) + n).astype(np.float32)))
+    return f32_to_bf16((o * np.float32(ls)).astype(np.float32))
+
+
+# ----------------------------------------------------------------------------
 # Synthetic inputs (the workload definitions) — torch CPU generators so CPU and
 # GPU see identical bits.
 # ----------------------------------------------------------------------------

@@ -85,3 +85,36 @@ def assert_topk_equivalent(probs, ids_a, w_a, ids_b, w_b, rtol=1e-5, boundary_rt
         for i, w in zip(ids_b[r].tolist(), np.asarray(w_b[r]).tolist()):
             if i in wa:
                 assert abs(w - wa[i]) <= rtol * abs(wa[i]) + 1e-9, f"row {r} id {i}: weight {w} vs {wa[i]}"
+
+
+# The feed-forward block's tail (two chained RMSNorms with bf16 roundings in
+# between): see the module docstring of tests/test_gpu_block.py for the bar.
+TAIL_MIN_EXACT = 0.999
+TAIL_MAX_ULP = 2
+TAIL_ABS = 2.0 ** -4
+
+
+def assert_tail_close(got_bits: np.ndarray, ref_bits: np.ndarray, ls: float, what: str = "") -> None:
+    got_bits = np.asarray(got_bits, dtype=np.uint16)
+    ref_bits = np.asarray(ref_bits, dtype=np.uint16)
+    assert got_bits.shape == ref_bits.shape
+    d = ulp_diff16(got_bits, ref_bits)
+    a = np.abs((got_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+               - (ref_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
+    exact = float((d == 0).mean())
+    ok = (d <= TAIL_MAX_ULP) | (a <= TAIL_ABS * abs(ls))
+    print(f"{what}: bit-exact {exact:.6f}, max ulp {int(d.max())}, max abs {a.max():.3g}, "
+          f"outside bar {int((~ok).sum())}", flush=True)
+    assert ok.all()
+    assert exact >= TAIL_MIN_EXACT
+
+
+class Fixed(torch.nn.Module):
+    """Stands in for a submodule whose output is given (attention, MLP, experts)."""
+
+    def __init__(self, out, as_tuple=False):
+        super().__init__()
+        self.out, self.as_tuple = out, as_tuple
+
+    def forward(self, *args, **kwargs):
+        return (self.out, None) if self.as_tuple else self.out

@@ -25,7 +25,8 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ("ksl_rmsnorm", "ksl_moe_align", "ksl_moe_w4a16_forward", "ksl_moe_layer_forward",
-              "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_moe_router", "ksl_version",
+              "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_moe_router", "ksl_moe_combine_post",
+              "ksl_moe_block_forward", "ksl_version",
               "ksl_status_string"):
         assert n in names
 
@@ -92,3 +93,32 @@ def test_router_rejects_bad_arguments_without_launching():
     assert L.ksl_moe_router(fake, 2, 2800, fake, fake, fake, 2, 1e-6, 256, 2800, 128, 8, fake, fake, fake, null) == 2
     # T = 0 is a no-op
     assert L.ksl_moe_router(null, 2, 2816, null, null, null, 2, 1e-6, 0, 2816, 128, 8, null, null, null, null) == 0
+
+
+def test_block_tail_entry_points_reject_bad_arguments_without_launching():
+    """Argument checks of ksl_moe_combine_post / ksl_moe_block_forward run on the host."""
+    L = load_mod("_lib").load()
+    P = ctypes.c_void_p
+    fake, null = P(1 << 20), P(0)
+    odd = P((1 << 20) + 8)
+
+    def post(T=256, tk=8, H=2816, h1=fake, res=fake, ls=null, ls_dt=2, wd=0, ys=2816, y=fake):
+        return L.ksl_moe_combine_post(fake, fake, fake, wd, T, tk, H, h1, 2816, res, 2816, fake, 1e-6, fake, 1e-6,
+                                      ls, ls_dt, y, ys, null)
+    assert post(T=0, h1=null, res=null, y=null) == 0          # no-op
+    assert post(res=null) == 1                                # residual required
+    assert post(ls=fake, ls_dt=1) == 1                        # layer scalar fp32 or bf16 only
+    assert post(wd=5) == 1                                    # unknown weight dtype
+    assert post(H=2820) == 2 and post(H=8200, ys=8200) == 2   # H % 8, H <= 8192
+    assert post(ys=2800) == 2                                 # stride below H
+    assert post(y=odd) == 3                                   # misaligned output
+
+    def block(T=256, H=2816, I=704, act=1, h1=fake, ws=null, wsb=0):
+        return L.ksl_moe_block_forward(fake, H, fake, 1e-6, fake, fake, 0, fake, fake, fake, fake, fake, fake,
+                                       T, 8, 128, H, I, act, h1, H, fake, 1e-6, fake, 1e-6, null, 2, fake, H,
+                                       ws, wsb, null)
+    assert block(I=700) == 2 and block(H=2800) == 2
+    assert block(act=9) == 1
+    assert block(h1=null) == 1
+    assert block() == 5                                       # workspace missing
+    assert block(T=0) == 0

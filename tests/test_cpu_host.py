@@ -77,3 +77,24 @@ def test_workload_shapes():
     assert torch.allclose(w.sum(-1), torch.ones(16))
     a, b = wl.make_routing(16, 4, 2, 2)
     assert torch.equal(a, ids) and torch.equal(b, w)  # seeded
+
+
+def test_moe_block_forward_checks_dtypes_and_patches_layers():
+    mb = load_mod("moe_block")
+    with pytest.raises(TypeError, match="bf16"):
+        mb.moe_block_forward(None, torch.zeros(4, 256), torch.zeros(4, 256))
+    with pytest.raises(ValueError, match="shapes"):
+        mb.moe_block_forward(None, torch.zeros(4, 256, dtype=torch.bfloat16), torch.zeros(4, 128, dtype=torch.bfloat16))
+
+    # only layers whose experts carry the packed buffers are rebound
+    class DiffusionGemmaDecoderTextLayer(torch.nn.Module):
+        def __init__(self, packed):
+            super().__init__()
+            self.experts = torch.nn.Module()
+            if packed:
+                self.experts.gu_q = torch.zeros(1, dtype=torch.uint8)
+
+    model = torch.nn.ModuleList([DiffusionGemmaDecoderTextLayer(True), DiffusionGemmaDecoderTextLayer(False)])
+    assert mb.patch_moe_blocks(model, verbose=False) == 1
+    assert model[0].forward.__func__ is mb.layer_forward
+    assert "forward" not in model[1].__dict__

@@ -12,7 +12,7 @@ import torch
 
 from oracle import moe_oracle as mo
 from oracle import oracle_c
-from tests._helpers import assert_topk_equivalent, bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
+from tests._helpers import Fixed, assert_topk_equivalent, bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
 
 
 def _bf16_row(x: torch.Tensor) -> np.ndarray:
@@ -372,3 +372,94 @@ def test_router_closed_forms():
     pes[7] = 2.0
     p, w, i = mo.router(x, ones_h, proj, pes, 1e-6, 1)
     assert i[2, 0] == 7 and w[2, 0] == 2.0
+
+
+# ------------------------------------------------------------------ block tail
+def _oracle_norm_forward(mod):
+    # the fused RMSNorm every DiffusionGemmaRMSNorm is patched to
+    # (kernels/load_w4_checkpoint.py:126-127); the oracle's rmsnorm restates it
+    def fwd(hs):
+        w = mod.weight.detach().float().numpy() if mod.with_scale else None
+        y = mo.rmsnorm(hs.detach().float().numpy().reshape(-1, hs.shape[-1]), w, mod.eps)
+        return bits_to_bf16_tensor(y).reshape(hs.shape)
+    return fwd
+
+
+def stock_layer_tail_case(T, H, seed, ls, ls_dtype, encoder=False):
+    """A transformers DiffusionGemma layer (bf16) whose attention, MLP and
+    experts return fixed tensors and whose norms are the fused RMSNorm. Returns
+    (layer output, m, h1, residual, layer)."""
+    from transformers.models.diffusion_gemma.configuration_diffusion_gemma import DiffusionGemmaTextConfig
+    from transformers.models.diffusion_gemma import modeling_diffusion_gemma as tfm
+    cfg = DiffusionGemmaTextConfig(num_experts=16, hidden_size=H, moe_intermediate_size=128, top_k_experts=4,
+                                   intermediate_size=384, num_attention_heads=2, num_key_value_heads=1,
+                                   head_dim=128, rms_norm_eps=1e-6, num_hidden_layers=2)
+    cls = tfm.DiffusionGemmaEncoderTextLayer if encoder else tfm.DiffusionGemmaDecoderTextLayer
+    lay = cls(cfg, 1).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for mod in lay.modules():
+            if isinstance(mod, tfm.DiffusionGemmaRMSNorm) and mod.with_scale:
+                mod.weight.copy_(1 + 0.2 * torch.randn(mod.weight.shape, generator=g))
+        lay.layer_scalar = torch.tensor([ls], dtype=ls_dtype)
+    for mod in lay.modules():
+        if isinstance(mod, tfm.DiffusionGemmaRMSNorm):
+            mod.forward = _oracle_norm_forward(mod)
+    hidden = torch.randn(1, T, H, generator=g).to(torch.bfloat16)
+    m = (10 * torch.randn(T, H, generator=g)).to(torch.bfloat16)
+    lay.self_attn = Fixed(torch.randn(1, T, H, generator=g).to(torch.bfloat16), as_tuple=True)
+    lay.mlp = Fixed((3 * torch.randn(1, T, H, generator=g)).to(torch.bfloat16))
+    lay.experts = Fixed(m)
+    seen = {}
+    lay.pre_feedforward_layernorm_2.register_forward_pre_hook(lambda mod, a: seen.__setitem__("res", a[0]))
+    lay.post_feedforward_layernorm_1.register_forward_hook(lambda mod, a, o: seen.__setitem__("h1", o))
+    with torch.no_grad():
+        out = lay(hidden)
+    return out, m, seen["h1"].reshape(T, H), seen["res"].reshape(T, H), lay
+
+
+@pytest.mark.parametrize("ls,ls_dtype,encoder", [(0.75, torch.bfloat16, False), (0.7071, torch.float32, False),
+                                                 (1.0, torch.bfloat16, True)])
+def test_block_tail_matches_stock_layer(ls, ls_dtype, encoder):
+    """TF DiffusionGemma{Decoder,Encoder}TextLayer.forward (modeling_diffusion_gemma.py:733-743,
+    :655-665) around fixed attention/MLP/expert outputs: bit for bit."""
+    T, H = 24, 256
+    out, m, h1, res, lay = stock_layer_tail_case(T, H, 41, ls, ls_dtype, encoder)
+    lsv = float(lay.layer_scalar.float()[0])
+    got = mo.block_tail(bf16_bits(m), h1.float().numpy(), res.float().numpy(),
+                        lay.post_feedforward_layernorm_2.weight.float().detach().numpy(),
+                        lay.post_feedforward_layernorm.weight.float().detach().numpy(), lsv, 1e-6, 1e-6)
+    assert np.array_equal(got, bf16_bits(out.reshape(T, H)))
+    # a plausible mix-up fails: the two norm weights swapped
+    bad = mo.block_tail(bf16_bits(m), h1.float().numpy(), res.float().numpy(),
+                        lay.post_feedforward_layernorm.weight.float().detach().numpy(),
+                        lay.post_feedforward_layernorm_2.weight.float().detach().numpy(), lsv, 1e-6, 1e-6)
+    assert not np.array_equal(bad, got)
+
+
+def test_block_tail_closed_forms():
+    g = np.random.default_rng(42)
+    T, H = 6, 128
+    bf = lambda a: mo.f32_to_bf16(np.asarray(a, np.float32))
+    m = bf(8 * g.standard_normal((T, H)))
+    h1 = mo.bf16_to_f32(bf(g.standard_normal((T, H))))
+    res = mo.bf16_to_f32(bf(g.standard_normal((T, H))))
+    w2 = mo.bf16_to_f32(bf(1 + 0.2 * g.standard_normal(H)))
+    wp = mo.bf16_to_f32(bf(1 + 0.2 * g.standard_normal(H)))
+    base = mo.block_tail(m, h1, res, w2, wp, 1.0, 0.0, 1e-6)
+    # the first norm is scale-free: with eps 0, 2*m gives the same bits
+    m2 = bf(2 * mo.bf16_to_f32(m))
+    assert np.array_equal(mo.block_tail(m2, h1, res, w2, wp, 1.0, 0.0, 1e-6), base)
+    # the layer scalar: 0 gives zeros, a power of two scales exactly
+    assert not mo.bf16_to_f32(mo.block_tail(m, h1, res, w2, wp, 0.0, 0.0, 1e-6)).any()
+    y2 = mo.block_tail(m, h1, res, w2, wp, 2.0, 0.0, 1e-6)
+    assert np.array_equal(mo.bf16_to_f32(y2), 2 * mo.bf16_to_f32(base))
+    # no expert output: the tail is residual + norm(h1)
+    z = mo.block_tail(np.zeros((T, H), np.uint16), h1, res, w2, wp, 1.0, 1e-6, 1e-6)
+    ref = bf(res + mo.bf16_to_f32(mo.rmsnorm(h1, wp, 1e-6)))
+    assert np.array_equal(z, ref)
+    # zero residual and hidden_states_1, unit weights: norm(norm(m)) = norm(m) to one ulp
+    ones = np.ones(H, np.float32)
+    zr = np.zeros((T, H), np.float32)
+    nn = mo.block_tail(m, zr, zr, ones, ones, 1.0, 0.0, 0.0)
+    assert ulp_diff16(nn, mo.rmsnorm(mo.bf16_to_f32(m), None, 0.0)).max() <= 1
