@@ -20,6 +20,13 @@
 //      expert is the original row order (stable).
 // Extra workgroups (blockIdx.x > 0) convert hidden to fp16 for the GEMMs,
 // in the gate/up activation order (act_store_index<128>).
+//
+// The compact routing (block_m = 1) of at most kFastRows rows, the layer's
+// case, takes a wider route: small workgroups each stage the keys in LDS once,
+// then one wave per expert (plus one for the dropped rows) counts the rows
+// below its expert (that count is the expert's first slot) and places its own
+// rows in row order with one wave scan (stable, the same result), with no
+// workgroup-wide scan and one barrier.
 #include "ksl_common.h"
 
 namespace ksl {
@@ -76,6 +83,109 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
                            IdxT* __restrict__ expert_ids, IdxT* __restrict__ inv,
                            int32_t* __restrict__ offsets);
 
+// 8 consecutive values (logical columns c0 .. c0+7) as fp16 in K-slot order
+// {0,4,1,5,2,6,3,7} at their gate/up activation position.
+__device__ __forceinline__ void store_act8(f16* __restrict__ row, int c0, const float (&f)[8]) {
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        o[2 * j] = static_cast<f16>(f[j]);
+        o[2 * j + 1] = static_cast<f16>(f[j + 4]);
+    }
+    *reinterpret_cast<f16x8*>(row + act_store_index<128>(c0)) = o;
+}
+
+constexpr int kFastRows = 4096;                           // routed rows of the barrier-free compact routing
+constexpr int kFastWaves = 4;                             // waves per workgroup of the fast kernels
+constexpr int kFastPad = kFastRows + kWave * 8;           // staged keys incl. padding to 8 per lane
+constexpr int kFastPer = kFastPad / (kFastWaves * kWave); // ids loaded per thread at most
+
+// Compact routing by the routing workgroups of the fast kernels. The
+// workgroup stages every key in LDS once (key = expert id, E for a dropped
+// id, E + 1 for padding past the last row); then wave `e` (0 <= e <= E)
+// routes expert e with no further barrier: lane l takes the rows
+// l*rpl .. l*rpl + rpl - 1 (rpl = ceil(Nexp / 64) rounded up to 8, read as
+// 16-byte groups of 8 keys), so row order is (lane, then position). The
+// expert's first slot is the number of rows with a smaller key (a wave sum of
+// per-lane counts); a lane's first slot adds the expert's rows held by the
+// lanes below it (a wave scan); each lane then places its own rows in order:
+// the stable order of the reference. Wave E writes inv = 0 for dropped rows,
+// offsets[E] and the unused tail slots (Nexp).
+__device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, int Nexp, int E,
+                                              int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv,
+                                              int32_t* __restrict__ offsets) {
+    __shared__ __attribute__((aligned(16))) uint16_t keys[kFastPad];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int e = blockIdx.x * kFastWaves + threadIdx.x / kWave;
+    const int rpl = ((Nexp + kWave - 1) / kWave + 7) & ~7;
+    const int npad = rpl * kWave;
+    // 1. keys into LDS: batches of 8 loads per thread, all issued before use
+    constexpr int kBatch = 8;
+    constexpr int kThreads = kFastWaves * kWave;
+#pragma unroll
+    for (int b = 0; b < kFastPer; b += kBatch) {
+        if (b * kThreads >= npad) break;
+        int64_t idv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int r = (b + i) * kThreads + static_cast<int>(threadIdx.x);
+            idv[i] = ids[r < Nexp ? r : 0];
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int r = (b + i) * kThreads + static_cast<int>(threadIdx.x);
+            const int64_t id = idv[i];
+            const int key = r >= Nexp ? E + 1 : ((id < 0 || id > E) ? E : static_cast<int>(id));
+            if (r < npad) keys[r] = static_cast<uint16_t>(key);
+        }
+    }
+    __syncthreads();
+    if (e > E) return;
+    // 2. this lane's rows: counts below and at e
+    const int r0 = lane * rpl;
+    const u32x4* kq = reinterpret_cast<const u32x4*>(keys + r0);
+    const int nq = rpl / 8;
+    int c_lt = 0, c_eq = 0;
+    for (int q = 0; q < nq; ++q) {
+        const u32x4 v = kq[q];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = static_cast<int>((v[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+            c_lt += k < e ? 1 : 0;
+            c_eq += k == e ? 1 : 0;
+        }
+    }
+    const int before = __ockl_wfred_add_i32(c_lt);
+    int incl = c_eq;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+    }
+    // 3. scatter in row order
+    int slot = before + incl - c_eq;
+    for (int q = 0; q < nq; ++q) {
+        const u32x4 v = kq[q];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = static_cast<int>((v[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+            if (k == e) {
+                const int r = r0 + q * 8 + j;
+                if (e < E) {
+                    sorted_rows[slot] = r;
+                    inv[r] = slot;
+                    ++slot;
+                } else {
+                    inv[r] = 0;
+                }
+            }
+        }
+    }
+    if (lane == 0) offsets[e] = before;
+    if (e == E)
+        for (int p = before + lane; p < Nexp; p += kWave) sorted_rows[p] = Nexp;
+}
+
 template <typename IdxT, int HD>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const int64_t* __restrict__ ids, RouteOut R, IdxT* __restrict__ sorted_rows,
@@ -96,16 +206,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
             const int64_t c0 = (v - t * vec_per_row) * 8;
             float f[8];
             load8<HD>(h + t * hidden_stride + c0, f);
-            f16x8 o;
-            o[0] = static_cast<f16>(f[0]);
-            o[1] = static_cast<f16>(f[4]);
-            o[2] = static_cast<f16>(f[1]);
-            o[3] = static_cast<f16>(f[5]);
-            o[4] = static_cast<f16>(f[2]);
-            o[5] = static_cast<f16>(f[6]);
-            o[6] = static_cast<f16>(f[3]);
-            o[7] = static_cast<f16>(f[7]);
-            *reinterpret_cast<f16x8*>(a16 + t * H + act_store_index<128>(static_cast<int>(c0))) = o;
+            store_act8(a16 + t * H, static_cast<int>(c0), f);
         }
         return;
     }
@@ -135,19 +236,56 @@ __global__ __launch_bounds__(kRouteThreads) void route_norm_kernel(
     for (int64_t row = static_cast<int64_t>(blockIdx.x - 1) * kRouteWaves + wave; row < T; row += nworkers) {
         f16* arow = a16 + row * H;
         rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true,
-                                      [&](int, int c0, const float (&v)[8]) {
-                                          f16x8 o;
-                                          o[0] = static_cast<f16>(v[0]);
-                                          o[1] = static_cast<f16>(v[4]);
-                                          o[2] = static_cast<f16>(v[1]);
-                                          o[3] = static_cast<f16>(v[5]);
-                                          o[4] = static_cast<f16>(v[2]);
-                                          o[5] = static_cast<f16>(v[6]);
-                                          o[6] = static_cast<f16>(v[3]);
-                                          o[7] = static_cast<f16>(v[7]);
-                                          *reinterpret_cast<f16x8*>(arow + act_store_index<128>(c0)) = o;
-                                      });
+                                      [&](int, int c0, const float (&v)[8]) { store_act8(arow, c0, v); });
     }
+}
+
+// Fast compact routing (at most kFastRows rows) and the activation prep in one
+// launch of kFastWaves-wave workgroups: workgroups below nrw route (wave =
+// expert), the rest convert hidden to fp16 (one row per wave).
+template <int HD>
+__global__ __launch_bounds__(kFastWaves * kWave) void route_fast_kernel(
+    const int64_t* __restrict__ ids, int Nexp, int E, int nrw, int32_t* __restrict__ sorted_rows,
+    int32_t* __restrict__ inv, int32_t* __restrict__ offsets, const void* __restrict__ hidden,
+    int64_t hidden_stride, int64_t T, int64_t H, f16* __restrict__ a16) {
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (static_cast<int>(blockIdx.x) < nrw) {
+        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets);
+        return;
+    }
+    const int64_t row = static_cast<int64_t>(blockIdx.x - nrw) * kFastWaves + wave;
+    if (row >= T) return;
+    typedef typename Elem<HD>::T HT;
+    const HT* h = static_cast<const HT*>(hidden) + row * hidden_stride;
+    for (int c0 = lane * 8; c0 < H; c0 += kWave * 8) {
+        float f[8];
+        load8<HD>(h + c0, f);
+        store_act8(a16 + row * H, c0, f);
+    }
+}
+
+// Fast compact routing fused with the RMSNorm -> fp16 activations (one row per
+// wave in the workgroups from nrw on).
+template <int XD, int WD, int NSTEP, bool HAS_W>
+__global__ __launch_bounds__(kFastWaves * kWave) void route_norm_fast_kernel(
+    const int64_t* __restrict__ ids, int Nexp, int E, int nrw, int32_t* __restrict__ sorted_rows,
+    int32_t* __restrict__ inv, int32_t* __restrict__ offsets, const void* __restrict__ xv, int64_t x_stride,
+    const void* __restrict__ wv, float eps, int64_t T, int64_t H, f16* __restrict__ a16) {
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (static_cast<int>(blockIdx.x) < nrw) {
+        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets);
+        return;
+    }
+    const int64_t row = static_cast<int64_t>(blockIdx.x - nrw) * kFastWaves + wave;
+    if (row >= T) return;
+    typedef typename Elem<XD>::T XT;
+    typedef typename Elem<WD>::T WT;
+    f16* arow = a16 + row * H;
+    rms_row<XD, WD, NSTEP, HAS_W>(static_cast<const XT*>(xv) + row * x_stride, static_cast<const WT*>(wv),
+                                  static_cast<int>(H), eps, lane, 6, true,
+                                  [&](int, int c0, const float (&v)[8]) { store_act8(arow, c0, v); });
 }
 
 template <typename IdxT>
@@ -329,6 +467,29 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
     }
     const int64_t Nexp = T * topk;
     f16* a = static_cast<f16*>(a16);
+    if (Nexp > 0 && Nexp <= kFastRows) {
+        const int nrw = static_cast<int>((E + 1 + kFastWaves - 1) / kFastWaves);
+        const int64_t nprep = a ? (T + kFastWaves - 1) / kFastWaves : 0;
+        const dim3 grid(static_cast<unsigned>(nrw + nprep)), block(kFastWaves * kWave);
+        switch (hd) {
+            case KSL_DTYPE_BF16:
+                hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_BF16>, grid, block, 0, st, ids, static_cast<int>(Nexp),
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                break;
+            case KSL_DTYPE_F16:
+                hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_F16>, grid, block, 0, st, ids, static_cast<int>(Nexp),
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                break;
+            case KSL_DTYPE_F32:
+                hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_F32>, grid, block, 0, st, ids, static_cast<int>(Nexp),
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                break;
+            default:
+                return KSL_ERR_ARG;
+        }
+        KSL_LAUNCH_CHECK();
+        return KSL_OK;
+    }
     // compact layout: block_m = 1; slots past offsets[E] hold Nexp, only the
     // first Nexp slots are materialised.
     switch (hd) {
@@ -352,6 +513,22 @@ template <int XD, int WD, bool HAS_W>
 int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32_t* sorted_rows, int32_t* inv,
                          int32_t* offsets, const void* x, int64_t xs, const void* w, float eps, int64_t T,
                          int64_t H, f16* a16, hipStream_t st) {
+    if (R.Nexp > 0 && R.Nexp <= kFastRows) {
+        const int nrw = (R.E + 1 + kFastWaves - 1) / kFastWaves;
+        const dim3 fgrid(static_cast<unsigned>(nrw + (T + kFastWaves - 1) / kFastWaves)), fblock(kFastWaves * kWave);
+        const int nexp = static_cast<int>(R.Nexp);
+#define KSL_RNF(NS)                                                                                          \
+    hipLaunchKernelGGL((route_norm_fast_kernel<XD, WD, NS, HAS_W>), fgrid, fblock, 0, st, ids, nexp, R.E, nrw, \
+                       sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16)
+        if (nstep <= 1) KSL_RNF(1);
+        else if (nstep <= 2) KSL_RNF(2);
+        else if (nstep <= 4) KSL_RNF(4);
+        else if (nstep <= 6) KSL_RNF(6);
+        else KSL_RNF(8);
+#undef KSL_RNF
+        KSL_LAUNCH_CHECK();
+        return KSL_OK;
+    }
     int64_t want = (T + kRouteWaves - 1) / kRouteWaves;
     if (want < 1) want = 1;
     if (want > 4096) want = 4096;

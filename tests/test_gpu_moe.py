@@ -105,7 +105,7 @@ def test_route_compact_and_activation_copy(gpu):
 
 
 ROUTE_CASES = [
-    # (T, tk, E, seed, dropped)  T*tk <= 4096: one wave per expert; above: one workgroup
+    # (T, tk, E, seed, dropped)  T*tk <= 4096: the wide route (a wave per expert); above: one workgroup
     (256, 8, 128, 23, False),
     (37, 3, 8, 24, True),
     (300, 2, 512, 25, True),
@@ -132,6 +132,50 @@ def test_route_compact_bit_exact(gpu, T, tk, E, seed, dropped):
     assert np.array_equal(_np(sr), ref_sr[:T * tk])
     assert np.array_equal(_np(inv), ref_inv)
     assert np.array_equal(_np(off), np.concatenate([[0], np.cumsum(counts)]))
+
+
+LAYER_ROUTE_CASES = [
+    # (T, tk, E, H, seed, dropped): routing + RMSNorm -> fp16 in one launch (ksl_moe_layer_route)
+    (256, 8, 128, 2816, 31, False),
+    (37, 3, 8, 256, 32, True),
+    (1, 8, 128, 2816, 33, False),
+    (600, 8, 128, 512, 34, True),
+]
+
+
+@pytest.mark.parametrize("T,tk,E,H,seed,dropped", LAYER_ROUTE_CASES)
+def test_layer_route_bit_exact(gpu, T, tk, E, H, seed, dropped):
+    """The layer's first launch: compact routing bit-exact vs the oracle and the
+    fp16 activations equal to fp16(fused_rmsnorm(x)) in the gate/up order."""
+    lib = load_pkg()._lib
+    frm = load_mod("fused_rmsnorm")
+    wl = load_mod("workloads")
+    ids, _ = wl.make_routing(T, E, tk, seed)
+    ids = ids.clone()
+    if dropped:
+        ids[0, 0] = E
+        ids[T // 2, tk - 1] = E + 3
+    x = wl.make_hidden(T, H, seed + 1, std=2.0)
+    nw = wl.make_norm_weight(H, seed + 2)
+    xg, nwg, idsg = x.to(gpu), nw.to(gpu), ids.to(gpu)
+    sr = torch.empty(T * tk, dtype=torch.int32, device=gpu)
+    off = torch.empty(E + 1, dtype=torch.int32, device=gpu)
+    inv = torch.empty(T * tk, dtype=torch.int32, device=gpu)
+    a16 = torch.empty(T, H, dtype=torch.float16, device=gpu)
+    print(f"layer_route T={T} topk={tk} E={E} H={H}", flush=True)
+    rc = lib.load().ksl_moe_layer_route(lib.ptr(idsg), T, tk, E, lib.ptr(sr), lib.ptr(off), lib.ptr(inv),
+                                        lib.ptr(xg), lib.DTYPE_BF16, H, lib.ptr(nwg), lib.DTYPE_BF16, 1e-6, H,
+                                        lib.ptr(a16), lib.stream_of(xg))
+    lib.check(rc, "ksl_moe_layer_route")
+    xn = frm.fused_rmsnorm(xg, nwg, 1e-6)
+    torch.cuda.synchronize()
+    ref_sr, _, _, ref_inv = mo.moe_align(ids.numpy(), 1, E)
+    flat = ids.numpy().reshape(-1)
+    counts = np.bincount(flat[flat < E], minlength=E)
+    assert np.array_equal(_np(sr), ref_sr[:T * tk])
+    assert np.array_equal(_np(inv), ref_inv)
+    assert np.array_equal(_np(off), np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(act_unperm(f16_bits(a16.cpu()), 128), f16_bits(xn.cpu().to(torch.float16)))
 
 
 # ----------------------------------------------------------- expert GEMMs
