@@ -307,6 +307,43 @@ def main() -> int:
             f"combine + 5 separate calls {unfused_us:.2f} us ({ndiff} of {T * H} elements differ by the "
             f"row-sum order); router + block forward {block_us:.2f} us (graph replay)")
 
+    # ---- the per-step sampler pass (not part of `value`) ---------------------
+    # [256 canvas tokens, 262144 vocab] fp32 logits, 3 * N(0, 1) (the reference's
+    # kill-test data): entropy alone, the Gumbel-max sample + argmax alone, and
+    # the one-pass step (both from one read).
+    sampler = None
+    if not args.skip_kernel_pass:
+        sops = importlib.import_module(f"{PKG}.fused_sampler_ops")
+        V = 262144
+        g = torch.Generator(device=dev)
+        g.manual_seed(17)
+        logits = 3.0 * torch.randn(T, V, generator=g, device=dev)
+        nbytes = logits.numel() * 4
+
+        def ev_us(fn, n):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(n):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) * 1e3 / n
+
+        ent_us = ev_us(lambda: sops.fused_entropy(logits), 20)
+        gum_us = ev_us(lambda: sops.gumbel_argmax_sample(logits, 1234), 10)
+        step_us = ev_us(lambda: sops.sample_step(logits, 1234), 10)
+        sampler = {"rows": T, "vocab": V, "logits_bytes": nbytes, "entropy_us": round(ent_us, 2),
+                   "entropy_GBps": round(nbytes / (ent_us * 1e-6) / 1e9, 1),
+                   "entropy_frac_of_hbm_peak": round(nbytes / (ent_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                   "gumbel_argmax_us": round(gum_us, 2), "sample_step_us": round(step_us, 2)}
+        log(f"[bench] sampler [{T}, {V}] fp32: entropy {ent_us:.1f} us ({sampler['entropy_GBps']:.0f} GB/s), "
+            f"gumbel+argmax {gum_us:.1f} us, one-pass step {step_us:.1f} us (the reference's two passes: "
+            f"{ent_us + gum_us:.1f} us here)")
+        del logits
+
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
@@ -374,6 +411,7 @@ def main() -> int:
             "kernels_us": {k: round(v["avg_us"], 3) for k, v in kernels.items()},
             "router_us": None if router_us is None else round(router_us, 3),
             "block_tail": tail,
+            "sampler": sampler,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

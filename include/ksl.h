@@ -1,6 +1,7 @@
-/* C ABI of the MI355X (gfx950) fused layer-kernel library: RMSNorm and the
- * W4A16 128-expert fused MoE forward of the DiffusionGemma block-diffusion
- * model.
+/* C ABI of the MI355X (gfx950) fused layer-kernel library of the DiffusionGemma
+ * block-diffusion model: RMSNorm and the W4A16 128-expert fused MoE forward,
+ * with the expert router before it, the feed-forward block's tail after it,
+ * and the per-step sampler pass (entropy, Gumbel-max sample, argmax).
  *
  * Every entry point takes raw device pointers, element counts and strides and
  * the HIP stream to launch on (hipStream_t passed as void*). Every entry point
@@ -207,6 +208,33 @@ int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_
                           int64_t h1_stride, const void* post2_w, float post2_eps, const void* post_w,
                           float post_eps, const void* layer_scalar, int ls_dtype, void* y,
                           int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- the per-step sampler pass (over [rows, V] logits, one read per call) ---- */
+
+/* Entropy (nats) of softmax(logits) per row, one pass: online running max,
+ * sum e^(x-m) and sum x e^(x-m). Replaces _entropy_kernel / fused_entropy
+ * (kernels/fused_sampler_ops.py:22-51). logits fp32, bf16 or fp16 [rows, V]
+ * (row stride row_stride elements, V < 2^31); entropy fp32 [rows]. Entries
+ * equal to -inf contribute nothing (torch's Categorical.entropy; the
+ * reference's kernel returns NaN for such rows). */
+int ksl_entropy(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, float* entropy,
+                void* stream);
+
+/* Gumbel-max sample and argmax per row. Replaces _gumbel_argmax_kernel /
+ * gumbel_argmax_sample (kernels/fused_sampler_ops.py:54-93): sampled = first
+ * index of the max of fp32(x + g), g = -log(-log(clamp(u, 1e-10, 1 - 1e-7))),
+ * u = tl.rand(seed + row, column), i.e. Triton's Philox4x32-10 stream (counter
+ * (column, 0, 0, 0), key = seed + row computed in int32 when seed fits int32,
+ * else int64, sign-extended); argmax = first index of the max of x. The same
+ * seed gives the reference's draws. sampled, argmax int64 [rows]. */
+int ksl_gumbel_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride,
+                      int64_t seed, int64_t* sampled, int64_t* argmax, void* stream);
+
+/* Both of the above in one read of the logits (the reference reads them twice
+ * per denoising step: the sample, then the sampler's entropy,
+ * kernels/fast_sampler.py:93-96). Not a reference entry point. */
+int ksl_sample_step(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, int64_t seed,
+                    int64_t* sampled, int64_t* argmax, float* entropy, void* stream);
 
 #ifdef __cplusplus
 }

@@ -9,15 +9,19 @@ Drop-in modules, named after the reference's kernel modules:
   router           router_forward, patch_routers (the expert router, the step before)
   moe_block        moe_block_forward, layer_forward, patch_moe_blocks (the MoE branch
                    with the layer's tail fused into the combine, the step after)
+  fused_sampler_ops  fused_entropy, gumbel_argmax_sample, sample_step (the per-step sampler pass)
+  fast_sampler     install, uninstall, stats (the generation-loop patches)
 All compute runs in libksl.so (hand-written HIP, C ABI in include/ksl.h).
 """
 from . import _lib
 from .fused_moe_w4 import moe_align
 from .fused_moe_w4_v2 import fused_moe_w4_v2
 from .fused_rmsnorm import fused_rmsnorm, patch_rmsnorms
+from .fused_sampler_ops import fused_entropy, gumbel_argmax_sample, sample_step
 from .pack_experts import fused_experts_forward
 from .moe_block import layer_forward, moe_block_forward, patch_moe_blocks
 from .router import patch_routers, router_forward
 
 __all__ = ["fused_rmsnorm", "patch_rmsnorms", "moe_align", "fused_moe_w4_v2", "fused_experts_forward",
-           "router_forward", "patch_routers", "moe_block_forward", "layer_forward", "patch_moe_blocks"]
+           "router_forward", "patch_routers", "moe_block_forward", "layer_forward", "patch_moe_blocks",
+           "fused_entropy", "gumbel_argmax_sample", "sample_step"]

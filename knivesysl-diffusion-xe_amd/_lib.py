@@ -50,6 +50,9 @@ SIGNATURES = {
     "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _F, _P, _F, _P, _I,
                                _P, _I64, _P, _SZ, _P], _I),
+    "ksl_entropy": ([_P, _I, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_gumbel_argmax": ([_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P], _I),
+    "ksl_sample_step": ([_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
 }
 
 _lock = threading.Lock()

@@ -10,6 +10,11 @@
  *  - orc_moe_align: kernels/fused_moe_w4.py:15-51, restated as a counting
  *    sort (stable by construction) instead of the reference's argsort, so
  *    that it is an independent check on the numpy restatement.
+ *  - orc_philox_first: the first output word of Philox4x32-10 for counters
+ *    (c, 0, 0, 0) and one key: the noise source of the Gumbel-max sampler
+ *    (kernels/fused_sampler_ops.py:67, tl.rand; Triton's philox_impl), the
+ *    same algorithm as oracle/sampler_oracle.py:philox4x32, in C for the
+ *    full-vocabulary rows (262144 columns) of the parity tests.
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so only the explicit fmaf
  * calls fuse).
@@ -135,4 +140,23 @@ int orc_moe_align(const int64_t* ids, int64_t Nexp, int64_t E, int64_t block_m,
 }
 
 /* Sanity probe used by the loader. */
+void orc_philox_first(const uint32_t* ctr, int64_t n, uint32_t key0, uint32_t key1, uint32_t* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t c0 = ctr[i], c1 = 0, c2 = 0, c3 = 0, k0 = key0, k1 = key1;
+        for (int r = 0; r < 10; ++r) {
+            const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+            const uint64_t p2 = (uint64_t)0xCD9E8D57u * c2;
+            const uint32_t n0 = (uint32_t)(p2 >> 32) ^ c1 ^ k0;
+            const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+            c1 = (uint32_t)p2;
+            c3 = (uint32_t)p0;
+            c0 = n0;
+            c2 = n2;
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        out[i] = c0;
+    }
+}
+
 int orc_version(void) { return 1; }

@@ -29,6 +29,8 @@ def lib():
         L.orc_combine.restype = ctypes.c_int
         L.orc_moe_align.argtypes = [p, i64, i64, i64, p, p, p]
         L.orc_moe_align.restype = ctypes.c_int
+        L.orc_philox_first.argtypes = [p, i64, ctypes.c_uint32, ctypes.c_uint32, p]
+        L.orc_philox_first.restype = None
         _LIB = L
     return _LIB
 
@@ -64,3 +66,11 @@ def moe_align(topk_ids: np.ndarray, block_m: int, E: int):
         raise IndexError("moe_align: negative expert id")
     assert rc == 0
     return sorted_rows, expert_ids, cap, inv
+
+
+def philox_first(ctr: np.ndarray, k0: int, k1: int) -> np.ndarray:
+    """First Philox4x32-10 output word for counters (c, 0, 0, 0), key (k0, k1)."""
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    out = np.empty_like(c)
+    lib().orc_philox_first(_ptr(c), c.size, k0 & 0xFFFFFFFF, k1 & 0xFFFFFFFF, _ptr(out))
+    return out
