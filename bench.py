@@ -112,13 +112,15 @@ def main() -> int:
     for exp in sets:
         v2._check_act(exp)
         v2._check_weights(exp, E, H, I)
+        v2.enable_tiled_down(exp)  # load-time repack of the down weights (same results)
+    torch.cuda.synchronize()
 
     def step(exp):
         # one C call: routing + RMSNorm + fp16 activations, gate/up, down, combine
         rc = L.ksl_moe_layer_forward(p(xg), lib.DTYPE_BF16, H, p(nwg), lib.DTYPE_BF16, 1e-6,
                                      p(idsg), p(wg), lib.DTYPE_F32,
                                      p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z),
-                                     T, TOPK, E, H, I, exp._ksl_act, p(y), lib.DTYPE_BF16, H,
+                                     lib.DN_LAYOUT_TILED, T, TOPK, E, H, I, exp._ksl_act, p(y), lib.DTYPE_BF16, H,
                                      p(ws), ws.numel(), st)
         if rc:
             lib.check(rc, "ksl_moe_layer_forward")
@@ -267,7 +269,8 @@ def main() -> int:
                 lib.check(rc, "ksl_moe_router")
             rc = L.ksl_moe_block_forward(p(xg), H, p(nwg), 1e-6, p(b_ids), p(b_w), lib.DTYPE_F32,
                                          p(exp0.gu_q), p(exp0.gu_s), p(exp0.gu_z), p(exp0.dn_q), p(exp0.dn_s),
-                                         p(exp0.dn_z), T, TOPK, E, H, I, exp0._ksl_act, p(t_h1), H, p(t_w2), 1e-6,
+                                         p(exp0.dn_z), lib.DN_LAYOUT_TILED, T, TOPK, E, H, I, exp0._ksl_act, p(t_h1), H,
+                                         p(t_w2), 1e-6,
                                          p(t_wp), 1e-6, p(t_ls), lib.DTYPE_BF16, p(b_y), H, p(ws), ws.numel(),
                                          stream)
             if rc:

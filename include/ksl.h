@@ -38,6 +38,10 @@ extern "C" {
 #define KSL_ACT_GELU_TANH 0 /* kernels/fused_moe_w4_v2.py:136-138 */
 #define KSL_ACT_SILU 1      /* SiLU-gated variant (act(g) = g * sigmoid(g)) */
 
+/* layouts of the down weights dn_q */
+#define KSL_DN_LAYOUT_REF 0   /* [E, H, I/2] as packed (kernels/w4a16.py:19-32) */
+#define KSL_DN_LAYOUT_TILED 1 /* regrouped per 16-row tile by ksl_moe_repack_down */
+
 /* Library version (bumped on ABI changes). */
 int ksl_version(void);
 
@@ -81,11 +85,13 @@ size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, in
  * zero-points are integers in [0, 15] as quantize_w4 writes them,
  * kernels/w4a16.py:28);
  * y: [T, H] of y_dtype with row stride y_stride. H % 128 == 0, I % 64 == 0
- * (fused_moe_w4_v2.py:327-328). */
+ * (fused_moe_w4_v2.py:327-328). dn_layout: KSL_DN_LAYOUT_REF, or
+ * KSL_DN_LAYOUT_TILED for dn_q regrouped by ksl_moe_repack_down (same
+ * results, faster weight stream). */
 int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_stride,
                           const int64_t* topk_ids, const void* topk_w, int w_dtype,
                           const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                          const uint8_t* dn_q, const void* dn_s, const void* dn_z,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
                           int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
                           void* y, int y_dtype, int64_t y_stride,
                           void* workspace, size_t workspace_bytes, void* stream);
@@ -103,7 +109,7 @@ int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_s
 int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
                           int norm_w_dtype, float eps, const int64_t* topk_ids, const void* topk_w,
                           int w_dtype, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout, int64_t T,
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                           int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -143,9 +149,20 @@ int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
 
 /* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
- * out3 fp16 [T*topk, H] row per sorted slot, natural column order. */
+ * out3 fp16 [T*topk, H] row per sorted slot, natural column order. dn_layout
+ * as in ksl_moe_w4a16_forward. */
 int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, void* stream);
+                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, int dn_layout, void* stream);
+
+/* Load-time repack of the down weights into the layout the down kernel loads
+ * (the row f3 of the loader: the reference's precedent is the preshuffled
+ * down pack, kernels/fused_moe_w4_v2.py:187-206). Out of place, same size as
+ * dn_q [E, H, I/2]. Within each 16-row tile (base address unchanged): unit u
+ * < I/128 is 1 KB, 16 bytes per lane l = c*16 + col: row col, bytes
+ * u*64 + c*16 .. +16; then for I % 128 == 64 a 512-byte tail, 8 bytes per
+ * lane: row col, bytes (I/128)*64 + c*8 .. +8. A pure permutation of bytes.
+ * H % 16 == 0, I % 64 == 0. */
+int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled, void* stream);
 
 /* Fixed-order top-k combine, no atomics: y[t,:] = fma-chain over k=0..topk-1
  * of fp32(w[t,k]) * fp32(out3[inv[t*topk+k], :]), rounded once to y_dtype.
@@ -203,7 +220,7 @@ int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_
 int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
                           const int64_t* topk_ids, const void* topk_w, int w_dtype,
                           const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout, int64_t T,
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, const void* h1,
                           int64_t h1_stride, const void* post2_w, float post2_eps, const void* post_w,
                           float post_eps, const void* layer_scalar, int ls_dtype, void* y,

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libksl.so")
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ACT_GELU_TANH, ACT_SILU = 0, 1
+DN_LAYOUT_REF, DN_LAYOUT_TILED = 0, 1
 
 _TORCH_TO_CODE = {
     torch.float32: DTYPE_F32,
@@ -35,19 +36,20 @@ SIGNATURES = {
     "ksl_rmsnorm": ([_P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _F, _P], _I),
     "ksl_moe_align": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
-    "ksl_moe_w4a16_forward": ([_P, _I, _I64, _P, _P, _I, _P, _P, _P, _P, _P, _P,
+    "ksl_moe_w4a16_forward": ([_P, _I, _I64, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _I64, _P, _P], _I),
     "ksl_moe_gateup_act": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P], _I),
-    "ksl_moe_down": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_moe_down": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I, _P], _I),
+    "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
-    "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P,
+    "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P], _I),
     "ksl_moe_router": ([_P, _I, _I64, _P, _P, _P, _I, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_combine_post": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _P, _F,
                               _P, _I, _P, _I64, _P], _I),
-    "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P,
+    "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _F, _P, _F, _P, _I,
                                _P, _I64, _P, _SZ, _P], _I),
     "ksl_entropy": ([_P, _I, _I64, _I64, _I64, _P, _P], _I),

@@ -19,7 +19,7 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
                   int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint);
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st);
+                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout);
 
 namespace {
 
@@ -314,7 +314,7 @@ extern "C" size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, in
 extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_stride,
                                      const int64_t* topk_ids, const void* topk_w, int w_dtype,
                                      const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z,
+                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
                                      int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
                                      void* y, int y_dtype, int64_t y_stride, void* workspace,
                                      size_t workspace_bytes, void* stream) {
@@ -322,6 +322,7 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
     if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
     if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (dn_layout != KSL_DN_LAYOUT_REF && dn_layout != KSL_DN_LAYOUT_TILED) return KSL_ERR_ARG;
     if (T == 0) return KSL_OK;
     const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
     if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
@@ -339,7 +340,7 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -348,7 +349,7 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
                                      int norm_w_dtype, float eps, const int64_t* topk_ids,
                                      const void* topk_w, int w_dtype, const uint8_t* gu_q,
                                      const void* gu_s, const void* gu_z, const uint8_t* dn_q,
-                                     const void* dn_s, const void* dn_z, int64_t T, int64_t topk,
+                                     const void* dn_s, const void* dn_z, int dn_layout, int64_t T, int64_t topk,
                                      int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                                      int64_t y_stride, void* workspace, size_t workspace_bytes,
                                      void* stream) {
@@ -356,6 +357,7 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
     if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
     if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (dn_layout != KSL_DN_LAYOUT_REF && dn_layout != KSL_DN_LAYOUT_TILED) return KSL_ERR_ARG;
     if (T == 0) return KSL_OK;
     const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
     if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
@@ -373,7 +375,7 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -381,8 +383,9 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
 extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
                                      const int64_t* topk_ids, const void* topk_w, int w_dtype,
                                      const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t T,
-                                     int64_t topk, int64_t E, int64_t H, int64_t I, int act, const void* h1,
+                                     const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                                     int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
+                                     const void* h1,
                                      int64_t h1_stride, const void* post2_w, float post2_eps,
                                      const void* post_w, float post_eps, const void* layer_scalar,
                                      int ls_dtype, void* y, int64_t y_stride, void* workspace,
@@ -391,6 +394,7 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
     if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
     if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
     if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (dn_layout != KSL_DN_LAYOUT_REF && dn_layout != KSL_DN_LAYOUT_TILED) return KSL_ERR_ARG;
     int rc = check_post(T, topk, H, w_dtype, h1, h1_stride, x, x_stride, post2_w, post_w, layer_scalar,
                         ls_dtype, y, y_stride);
     if (rc || T == 0) return rc;
@@ -410,7 +414,7 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
     if (rc) return rc;
     return launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, x, x_stride, post2_w,
                                post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);
@@ -424,7 +428,7 @@ extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t t
                            norm_w_dtype, eps, H, a16, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int ksl_version(void) { return 1; }
+extern "C" int ksl_version(void) { return 2; }
 
 extern "C" const char* ksl_status_string(int status) {
     switch (status) {

@@ -462,6 +462,18 @@ constexpr int kDnWaves = 11;
 constexpr int kDnThreads = kDnWaves * kWave;
 constexpr int kDnMaxG = 16;  // I <= 1024
 
+// Down weight layouts (dn_layout of the C ABI):
+//   reference: dn_q [E, H, I/2], one row per output column;
+//   tiled    : the same bytes regrouped per 16-row tile (the tile's base
+//              address unchanged) in the order lanes load them: unit u
+//              (u < I/128) is 64 lanes x 16 B, lane l = c*16 + col holding
+//              row col, bytes u*64 + c*16 .. +16; then, when I % 128 == 64, the
+//              tail: 64 lanes x 8 B, lane l holding row col, bytes
+//              (I/128)*64 + c*8 .. +8. Every load instruction then reads 1 KB
+//              (512 B for the tail) of contiguous memory instead of 16 row
+//              pieces of 64 B; the values, and so the results, are the same.
+enum DnLayout { kDnRef = KSL_DN_LAYOUT_REF, kDnTiled = KSL_DN_LAYOUT_TILED };
+
 struct DnArgs {
     const f16* out2;
     const int32_t* offsets;
@@ -492,15 +504,26 @@ struct DnW {
 // them before dn_wait_w, so a buffer enters the tile loop only once complete
 // and is otherwise loaded and used inside one loop iteration pair (checked in
 // the generated code: no register copies of a loading buffer).
-template <int G2, bool TAIL>
-__device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* rowp, int c) {
-    const uint8_t* p = rowp + c * 16;
+template <int G2, bool TAIL, int LAYOUT>
+__device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* tbase, int col, int c, int rb) {
+    if constexpr (LAYOUT == kDnTiled) {
+        const uint8_t* p = tbase + (c * 16 + col) * 16;
 #pragma unroll
-    for (int g2 = 0; g2 < G2; ++g2)
-        asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w.q[g2]) : "v"(p), "i"(g2 * 64) : "memory");
-    if constexpr (TAIL) {
-        const uint8_t* pt = rowp + G2 * 64 + c * 8;
-        asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
+        for (int g2 = 0; g2 < G2; ++g2)
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(w.q[g2]) : "v"(p + g2 * 1024) : "memory");
+        if constexpr (TAIL) {
+            const uint8_t* pt = tbase + G2 * 1024 + (c * 16 + col) * 8;
+            asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
+        }
+    } else {
+        const uint8_t* p = tbase + col * rb + c * 16;
+#pragma unroll
+        for (int g2 = 0; g2 < G2; ++g2)
+            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w.q[g2]) : "v"(p), "i"(g2 * 64) : "memory");
+        if constexpr (TAIL) {
+            const uint8_t* pt = tbase + col * rb + G2 * 64 + c * 8;
+            asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
+        }
     }
 }
 
@@ -619,7 +642,7 @@ __device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a
 // last tile they repeat it: an L2 hit), a repeated tile's stores are dropped,
 // so between a buffer's loads and its use exactly the other buffer's loads and
 // one tile's 4*MT stores are issued (on entry w0 has landed already).
-template <int G2, bool TAIL, int MT>
+template <int G2, bool TAIL, int MT, int LAYOUT>
 __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, const uint8_t* wrow, int rb,
                                          int nmine, int wave, const char* a_lds, const f16* s_lds,
                                          const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int colw, int mrows,
@@ -628,18 +651,18 @@ __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, c
     for (int k = 0; k < nmine; k += 2) {
         const int k1 = k + 1 < nmine ? k + 1 : nmine - 1;
         const int k2 = k + 2 < nmine ? k + 2 : nmine - 1;
-        dn_load_w<G2, TAIL>(w1, wrow + static_cast<int64_t>(wave + k1 * kDnWaves) * 16 * rb, c);
+        dn_load_w<G2, TAIL, LAYOUT>(w1, wrow + static_cast<int64_t>(wave + k1 * kDnWaves) * 16 * rb, col, c, rb);
         dn_wait_w<kAfter>(w0);
         dn_do_tile<G2, TAIL, MT>(w0, a_lds, s_lds, z_lds, out, H, wave + k * kDnWaves, colw, true, mrows, col, c,
                                  fo, kn);
-        dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave + k2 * kDnWaves) * 16 * rb, c);
+        dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave + k2 * kDnWaves) * 16 * rb, col, c, rb);
         dn_wait_w<kAfter>(w1);
         dn_do_tile<G2, TAIL, MT>(w1, a_lds, s_lds, z_lds, out, H, wave + k1 * kDnWaves, colw, k + 1 < nmine, mrows,
                                  col, c, fo, kn);
     }
 }
 
-template <int G2, bool TAIL>
+template <int G2, bool TAIL, int LAYOUT>
 __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -663,7 +686,7 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     f16* z_lds = s_lds + ncols * G;
     const int64_t row0 = static_cast<int64_t>(e) * A.H + col0;  // first dn row of the workgroup
     const int rb = A.I >> 1;
-    const uint8_t* wrow = A.dn_q + (row0 + col) * rb;  // this lane's row in tile 0
+    const uint8_t* wrow = A.dn_q + row0 * rb;  // the workgroup's first tile
     // 1. scale / zero rows and the first chunk's activations into LDS
     {
         const int nq = ncols * G / 8;  // 16-byte chunks per block
@@ -678,7 +701,7 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     }
     // 2. the first tile's weights, then wait for the LDS copies only
     DnW<G2, TAIL> w0, w1;
-    if (wave < ntiles) dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, c);
+    if (wave < ntiles) dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, col, c, rb);
     vm_wait<0>();
     dma_barrier();
     const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDnWaves + 1 : 0;
@@ -687,29 +710,56 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
         if (m0 > 0) {
             __syncthreads();  // every wave is done with the previous chunk's activations
             dn_stage_a<G2, TAIL>(A, a_lds, start, m0, mrows, mrows > 16 ? 2 : 1, wave, rr, ch);
-            if (wave < ntiles) dn_load_w<G2, TAIL>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, c);
+            if (wave < ntiles) dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, col, c, rb);
             vm_wait<0>();
             dma_barrier();
         }
         const __amdgpu_buffer_rsrc_t out =
             raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
         if (mrows > 16)
-            dn_tiles<G2, TAIL, 2>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
+            dn_tiles<G2, TAIL, 2, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
                                   fo, kn);
         else
-            dn_tiles<G2, TAIL, 1>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
+            dn_tiles<G2, TAIL, 1, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
                                   fo, kn);
     }
     vm_wait<0>();  // the last (repeated) prefetch lands before the wave ends
 }
 
 template <int G2, bool TAIL>
-int launch_down_g(const DnArgs& A, unsigned grid, size_t lds, hipStream_t st) {
-    static const bool attr = set_max_lds(reinterpret_cast<const void*>(&down_kernel<G2, TAIL>));
+int launch_down_g(const DnArgs& A, unsigned grid, size_t lds, int layout, hipStream_t st) {
+    static const bool attr = set_max_lds(reinterpret_cast<const void*>(&down_kernel<G2, TAIL, kDnRef>)) &&
+                             set_max_lds(reinterpret_cast<const void*>(&down_kernel<G2, TAIL, kDnTiled>));
     (void)attr;
-    hipLaunchKernelGGL((down_kernel<G2, TAIL>), dim3(grid), dim3(kDnThreads), lds, st, A);
+    if (layout == kDnTiled)
+        hipLaunchKernelGGL((down_kernel<G2, TAIL, kDnTiled>), dim3(grid), dim3(kDnThreads), lds, st, A);
+    else
+        hipLaunchKernelGGL((down_kernel<G2, TAIL, kDnRef>), dim3(grid), dim3(kDnThreads), lds, st, A);
     KSL_LAUNCH_CHECK();
     return KSL_OK;
+}
+
+// The tiled down layout from the reference one: one thread per 16-byte unit
+// (8-byte tail unit) of the output.
+__global__ __launch_bounds__(256) void repack_down_kernel(const uint8_t* __restrict__ src,
+                                                           uint8_t* __restrict__ dst, int64_t ntiles, int rb,
+                                                           int g2n, int tail) {
+    const int per_tile = g2n * kWave + (tail ? kWave : 0);
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= ntiles * per_tile) return;
+    const int64_t t = i / per_tile;
+    const int k = static_cast<int>(i - t * per_tile);
+    const uint8_t* tb = src + t * 16 * rb;
+    uint8_t* ob = dst + t * 16 * rb;
+    if (k < g2n * kWave) {
+        const int u = k / kWave, l = k - u * kWave, c = l >> 4, col = l & 15;
+        *reinterpret_cast<u32x4*>(ob + u * 1024 + l * 16) =
+            *reinterpret_cast<const u32x4*>(tb + col * rb + u * 64 + c * 16);
+    } else {
+        const int l = k - g2n * kWave, c = l >> 4, col = l & 15;
+        *reinterpret_cast<u32x2*>(ob + g2n * 1024 + l * 8) =
+            *reinterpret_cast<const u32x2*>(tb + col * rb + g2n * 64 + c * 8);
+    }
 }
 
 // ------------------------------------------------------ down, per-wave DMA
@@ -950,8 +1000,9 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st) {
+                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout) {
     if (!out2 || !offsets || !dn_q || !dn_s || !dn_z || !out3) return KSL_ERR_ARG;
+    if (layout != kDnRef && layout != kDnTiled) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
     if (H % 64 != 0 || I % 64 != 0 || I > 64 * kDnMaxG || H >= (1 << 24) || E >= (1 << 24)) return KSL_ERR_SHAPE;
     if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(out2) % 16 ||
@@ -981,7 +1032,7 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     const int64_t grid = E * nsplit;
     if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const size_t lds = dn_lds_bytes(G, static_cast<int>(tpw * 16));
-    if (kDownDmaTiles && G <= 12) {
+    if (kDownDmaTiles && layout == kDnRef && G <= 12) {
         // per-wave DMA tiles (static LDS, 8 waves): its own split, same rule
         int64_t ns = std::max<int64_t>(1, std::min<int64_t>((device_cus() + E - 1) / E, te));
         const int64_t tp = (te + ns - 1) / ns;
@@ -1000,7 +1051,7 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     }
     switch (G) {
 #define KSL_DN_CASE(GG) \
-    case GG: return launch_down_g<GG / 2, (GG % 2) != 0>(A, static_cast<unsigned>(grid), lds, st);
+    case GG: return launch_down_g<GG / 2, (GG % 2) != 0>(A, static_cast<unsigned>(grid), lds, layout, st);
         KSL_DN_CASE(1) KSL_DN_CASE(2) KSL_DN_CASE(3) KSL_DN_CASE(4) KSL_DN_CASE(5) KSL_DN_CASE(6)
         KSL_DN_CASE(7) KSL_DN_CASE(8) KSL_DN_CASE(9) KSL_DN_CASE(10) KSL_DN_CASE(11) KSL_DN_CASE(12)
         KSL_DN_CASE(13) KSL_DN_CASE(14) KSL_DN_CASE(15) KSL_DN_CASE(16)
@@ -1020,7 +1071,26 @@ extern "C" int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, c
 
 extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q,
                             const void* dn_s, const void* dn_z, int64_t E, int64_t H, int64_t I,
-                            void* out3, void* stream) {
+                            void* out3, int dn_layout, void* stream) {
     return ksl::launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3,
-                            static_cast<hipStream_t>(stream));
+                            static_cast<hipStream_t>(stream), dn_layout);
+}
+
+extern "C" int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled,
+                                   void* stream) {
+    using namespace ksl;
+    if (E <= 0 || H <= 0 || I <= 0 || H % 16 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (!dn_q || !dn_q_tiled) return KSL_ERR_ARG;
+    if (dn_q == dn_q_tiled) return KSL_ERR_ARG;  // out of place
+    if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(dn_q_tiled) % 16) return KSL_ERR_ALIGN;
+    const int64_t ntiles = E * (H / 16);
+    const int g2n = static_cast<int>(I / 128), tail = (I % 128) != 0;
+    const int64_t n = ntiles * (g2n * kWave + (tail ? kWave : 0));
+    const int64_t grid = (n + 255) / 256;
+    if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    hipLaunchKernelGGL(repack_down_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), dn_q, dn_q_tiled, ntiles, static_cast<int>(I / 2), g2n,
+                       tail);
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }

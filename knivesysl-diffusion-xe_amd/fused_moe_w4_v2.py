@@ -19,7 +19,9 @@ Differences from the reference, on purpose:
 - SiLU-gated experts are supported next to tanh-GELU (the reference asserts
   tanh-GELU, :291-308, :332).
 - The preshuffled down pack (MOE_NS, :180-245) is not used; `dn_ns` modules
-  are rejected.
+  are rejected. Its counterpart here is enable_tiled_down: the same bytes
+  regrouped in the order the down kernel loads them (same results, faster
+  weight stream), flagged by `dn_tiled`.
 - zero-points must be integers in [0, 15] (what quantize_w4 writes,
   kernels/w4a16.py:28); checked once per module.
 """
@@ -110,6 +112,44 @@ def _check_weights(exp, E, H, I) -> None:
     exp._ksl_weights_checked = True
 
 
+def dn_layout(exp) -> int:
+    return _lib.DN_LAYOUT_TILED if getattr(exp, "dn_tiled", False) else _lib.DN_LAYOUT_REF
+
+
+@torch.no_grad()
+def tiled_down(dn_q: torch.Tensor) -> torch.Tensor:
+    """dn_q [E, H, I/2] uint8 (reference layout) -> a new tensor of the same
+    shape in the tiled layout (ksl_moe_repack_down)."""
+    E, H, Ih = dn_q.shape
+    if not dn_q.is_cuda or dn_q.dtype != torch.uint8 or not dn_q.is_contiguous():
+        raise ValueError("dn_q must be a contiguous uint8 tensor on the GPU")
+    out = torch.empty_like(dn_q)
+    rc = _lib.load().ksl_moe_repack_down(_lib.ptr(dn_q), E, H, 2 * Ih, _lib.ptr(out), _lib.stream_of(dn_q))
+    _lib.check(rc, "ksl_moe_repack_down")
+    return out
+
+
+def enable_tiled_down(exp, cache: dict | None = None):
+    """Swap exp.dn_q to the tiled layout in place (idempotent via the dn_tiled
+    flag), as the reference's enable_ns_down swaps in its preshuffled pack
+    (kernels/fused_moe_w4_v2.py:200-206). `cache` maps an original buffer to its
+    repacked tensor, so modules that share one dn_q (the encoder and decoder
+    experts of a layer, kernels/load_w4_checkpoint.py:56-59) keep sharing one."""
+    if getattr(exp, "dn_tiled", False):
+        return exp
+    if getattr(exp, "dn_ns", False):
+        raise NotImplementedError("the preshuffled down pack (dn_ns) cannot be tiled; keep dn_q as [E, H, I/2]")
+    key = (exp.dn_q.data_ptr(), str(exp.dn_q.device))
+    t = None if cache is None else cache.get(key)
+    if t is None:
+        t = tiled_down(exp.dn_q)
+        if cache is not None:
+            cache[key] = t
+    exp.dn_q = t
+    exp.dn_tiled = True
+    return exp
+
+
 def moe_workspace(T: int, tk: int, E: int, H: int, I: int, device) -> torch.Tensor:
     nbytes = int(_lib.load().ksl_moe_workspace_bytes(T, tk, E, H, I))
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -149,7 +189,7 @@ def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: t
         _lib.ptr(hidden), _lib.dtype_code(hidden.dtype), hidden.stride(0),
         _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
         _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
-        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp),
         T, tk, E, K, I, exp._ksl_act,
         _lib.ptr(y), _lib.dtype_code(y_dtype), y.stride(0),
         _lib.ptr(workspace), workspace.numel(), _lib.stream_of(hidden))

@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fused_moe_w4_v2 import _check_act, _check_weights, fused_moe_w4_v2, moe_workspace
+from .fused_moe_w4_v2 import _check_act, _check_weights, dn_layout, fused_moe_w4_v2, moe_workspace
 from .fused_rmsnorm import fused_rmsnorm
 
 STAGES = ("route_norm", "gateup", "down", "combine")
@@ -58,7 +58,7 @@ def moe_layer(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float, exp, top
         _lib.dtype_code(nw.dtype) if nw is not None else _lib.DTYPE_BF16, float(eps),
         _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
         _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
-        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp),
         T, tk, E, H, I, exp._ksl_act, _lib.ptr(y), _lib.dtype_code(y.dtype), y.stride(0),
         _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x))
     _lib.check(rc, "ksl_moe_layer_forward")
@@ -113,7 +113,7 @@ class LayerRunner:
         if ev:
             ev[2].record()
         rc = L.ksl_moe_down(p(self.out2), p(self.offsets), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z), E, H, I,
-                            p(self.out3), st)
+                            p(self.out3), dn_layout(exp), st)
         _lib.check(rc, "ksl_moe_down")
         if ev:
             ev[3].record()

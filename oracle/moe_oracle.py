@@ -127,6 +127,40 @@ def dequant_w4(packed: np.ndarray, scale: np.ndarray, zero: np.ndarray, gs: int)
     return W.reshape(lead + (K,)).astype(np.float16)
 
 
+def tile_down(dn_q: np.ndarray) -> np.ndarray:
+    """The tiled down layout (the load-time repack of this build; the
+    reference keeps [E, H, I/2] and repacks only for its own kernel,
+    kernels/fused_moe_w4_v2.py:187-206). Per 16-row tile, same base: units
+    u < I/128 of 64 lanes x 16 B (lane c*16 + col: row col, bytes
+    u*64 + c*16 .. +16), then for I % 128 == 64 a tail of 64 lanes x 8 B
+    (row col, bytes (I/128)*64 + c*8 .. +8)."""
+    E, H, Ih = dn_q.shape
+    g2 = Ih // 64
+    t = dn_q.reshape(E, H // 16, 16, Ih)
+    main = t[..., :g2 * 64].reshape(E, H // 16, 16, g2, 4, 16).transpose(0, 1, 3, 4, 2, 5).reshape(E, H // 16, -1)
+    tail = t[..., g2 * 64:].reshape(E, H // 16, 16, -1, 8).transpose(0, 1, 3, 2, 4).reshape(E, H // 16, -1)
+    return np.concatenate([main, tail], axis=-1).reshape(E, H, Ih)
+
+
+def untile_down(tiled: np.ndarray, I: int) -> np.ndarray:
+    """Inverse of tile_down: byte b of tile row r is found at its lane unit."""
+    E, H, Ih = tiled.shape
+    g2 = I // 128
+    out = np.empty_like(tiled)
+    flat = tiled.reshape(E, H // 16, 16 * Ih)
+    for r in range(16):
+        for b in range(Ih):
+            if b < g2 * 64:
+                u, c, k = b // 64, (b % 64) // 16, b % 16
+                src = u * 1024 + (c * 16 + r) * 16 + k
+            else:
+                bb = b - g2 * 64
+                c, k = bb // 8, bb % 8
+                src = g2 * 1024 + (c * 16 + r) * 8 + k
+            out.reshape(E, H // 16, 16, Ih)[:, :, r, b] = flat[:, :, src]
+    return out
+
+
 # ----------------------------------------------------------------------------
 # Routing metadata — kernels/fused_moe_w4.py:15-51 (moe_align)
 # ----------------------------------------------------------------------------

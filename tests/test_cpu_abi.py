@@ -73,8 +73,13 @@ def test_validation_returns_before_device_work(L):
     assert L.ksl_moe_gateup_act(P((1 << 20) + 8), fake, fake, 256, 8, fake, fake, fake, 128, 2816, 704, 1, fake,
                                 null) == 3
     # down: I not a multiple of 64, I above 1024
-    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, fake, null) == 2
-    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, fake, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, fake, 0, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, fake, 0, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, fake, 7, null) == 1   # unknown layout
+    # repack: shapes, in-place refused, alignment
+    assert L.ksl_moe_repack_down(fake, 128, 2816, 700, P((1 << 21)), null) == 2
+    assert L.ksl_moe_repack_down(fake, 128, 2816, 704, fake, null) == 1
+    assert L.ksl_moe_repack_down(P((1 << 20) + 8), 128, 2816, 704, P(1 << 21), null) == 3
     # align: E above the routing limit
     assert L.ksl_moe_align(fake, 4, 8, 4096, 32, fake, fake, fake, null) == 2
 
@@ -113,12 +118,13 @@ def test_block_tail_entry_points_reject_bad_arguments_without_launching():
     assert post(ys=2800) == 2                                 # stride below H
     assert post(y=odd) == 3                                   # misaligned output
 
-    def block(T=256, H=2816, I=704, act=1, h1=fake, ws=null, wsb=0):
-        return L.ksl_moe_block_forward(fake, H, fake, 1e-6, fake, fake, 0, fake, fake, fake, fake, fake, fake,
+    def block(T=256, H=2816, I=704, act=1, h1=fake, ws=null, wsb=0, layout=0):
+        return L.ksl_moe_block_forward(fake, H, fake, 1e-6, fake, fake, 0, fake, fake, fake, fake, fake, fake, layout,
                                        T, 8, 128, H, I, act, h1, H, fake, 1e-6, fake, 1e-6, null, 2, fake, H,
                                        ws, wsb, null)
     assert block(I=700) == 2 and block(H=2800) == 2
     assert block(act=9) == 1
+    assert block(layout=2) == 1
     assert block(h1=null) == 1
     assert block() == 5                                       # workspace missing
     assert block(T=0) == 0

@@ -463,3 +463,25 @@ def test_block_tail_closed_forms():
     zr = np.zeros((T, H), np.float32)
     nn = mo.block_tail(m, zr, zr, ones, ones, 1.0, 0.0, 0.0)
     assert ulp_diff16(nn, mo.rmsnorm(mo.bf16_to_f32(m), None, 0.0)).max() <= 1
+
+
+
+# ------------------------------------------------------------------ tiled down layout
+def test_tile_down_known_answer_and_inverse():
+    """Hand-checked positions of the tiled layout (I = 192: one 1 KB unit and
+    a 512 B tail per 16-row tile) and the inverse round trip for I = 704 / 256."""
+    E, H, I = 1, 32, 192
+    q = np.arange(E * H * I // 2, dtype=np.int64).reshape(E, H, I // 2)
+    t = mo.tile_down(q)
+    flat = t.reshape(-1)
+    rb = I // 2  # 96 bytes per row
+    # tile 0, unit 0, lane c*16 + col = 1*16 + 3 (row 3, bytes 16..31) starts at byte 19*16
+    assert flat[19 * 16] == q[0, 3, 16] and flat[19 * 16 + 15] == q[0, 3, 31]
+    # tail of tile 0: lane 2*16 + 5 (row 5, bytes 64 + 16 .. +8) at 1024 + 37*8
+    assert flat[1024 + 37 * 8] == q[0, 5, 64 + 16] and flat[1024 + 37 * 8 + 7] == q[0, 5, 64 + 23]
+    # tile 1 keeps its base address (16 rows later)
+    assert flat[16 * rb] == q[0, 16, 0]
+    assert sorted(flat.tolist()) == list(range(q.size))  # a permutation
+    for I2 in (704, 256):
+        qq = np.random.default_rng(I2).integers(0, 256, size=(2, 48, I2 // 2)).astype(np.uint8)
+        assert np.array_equal(mo.untile_down(mo.tile_down(qq), I2), qq)

@@ -194,7 +194,7 @@ def _stage_run(gpu, exp, hidden, ids, act):
                               lib.ptr(exp.gu_z), E, H, I, act, lib.ptr(out2), st)
     lib.check(rc, "ksl_moe_gateup_act")
     rc = L.ksl_moe_down(lib.ptr(out2), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
-                        E, H, I, lib.ptr(out3), st)
+                        E, H, I, lib.ptr(out3), lib.DN_LAYOUT_REF, st)
     lib.check(rc, "ksl_moe_down")
     torch.cuda.synchronize()
     return sr, off, inv, out2, out3
@@ -370,3 +370,45 @@ def test_prefill_8192_zipf_sampled_tokens(gpu):
     mx, mean = norm_err(y[sample].float().numpy(), ref_b)
     print(f"prefill sample: norm max {mx:.2e} mean {mean:.2e}")
     assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+
+
+
+# ----------------------------------------------------------- tiled down layout (load-time repack)
+@pytest.mark.parametrize("E,H,I", [(128, 2816, 704), (4, 256, 128), (3, 512, 1024), (2, 64, 64)])
+def test_repack_down_bit_exact(gpu, E, H, I):
+    v2 = load_mod("fused_moe_w4_v2")
+    g = torch.Generator().manual_seed(E + H + I)
+    q = torch.randint(0, 256, (E, H, I // 2), generator=g, dtype=torch.uint8)
+    t = v2.tiled_down(q.to(gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(t), mo.tile_down(q.numpy()))
+
+
+@pytest.mark.parametrize("T,tk,E,H,I,seed", [(256, 8, 128, 2816, 704, 81), (40, 4, 16, 512, 256, 82)])
+def test_tiled_down_forward_is_bit_identical(gpu, T, tk, E, H, I, seed):
+    """The MoE forward and the staged down on the repacked weights equal the
+    reference layout bit for bit; repack_experts keeps shared buffers shared."""
+    wl = load_mod("workloads")
+    v2 = load_mod("fused_moe_w4_v2")
+    pe = load_mod("pack_experts")
+    x, _, ids, w = wl.layer_inputs(T, seed, E=E, k=tk, H=H)
+    exp = wl.make_experts(E, H, I, seed + 1, device=gpu)
+    xg, idsg, wg = x.to(gpu), ids.to(gpu), w.to(gpu)
+    y_ref = v2.fused_moe_w4_v2(xg, exp, idsg, wg)
+    exp_t = wl.Experts(exp.gu_q, exp.gu_s, exp.gu_z, exp.dn_q, exp.dn_s, exp.dn_z, exp.act_fn)
+    v2.enable_tiled_down(exp_t)
+    assert exp_t.dn_tiled and exp_t.dn_q.data_ptr() != exp.dn_q.data_ptr()
+    y_t = v2.fused_moe_w4_v2(xg, exp_t, idsg, wg)
+    torch.cuda.synchronize()
+    assert torch.equal(y_ref.view(torch.int16), y_t.view(torch.int16))
+    # two modules sharing one set of buffers (the encoder and decoder experts of a layer)
+    a = torch.nn.Module()
+    b = torch.nn.Module()
+    for k in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z"):
+        a.register_buffer(k, getattr(exp, k), persistent=False)
+        b.register_buffer(k, getattr(exp, k), persistent=False)
+    model = torch.nn.ModuleList([a, b])
+    assert pe.repack_experts(model, verbose=False) == 2
+    assert a.dn_q.data_ptr() == b.dn_q.data_ptr() and a.dn_tiled and b.dn_tiled
+    assert torch.equal(a.dn_q, exp_t.dn_q)
+    assert pe.repack_experts(model, verbose=False) == 2 and a.dn_q.data_ptr() == b.dn_q.data_ptr()  # idempotent
