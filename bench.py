@@ -36,6 +36,7 @@ PKG = "knivesysl-diffusion-xe_amd"
 
 METRIC = "µs per RMSNorm+W4A16 MoE layer at 256-tok canvas; achieved HBM GB/s (% peak)"
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16 MFMA, MI355X
 
 T, TOPK, E, H, I = 256, 8, 128, 2816, 704
 GU_EXPERT_BYTES = 2 * I * (H // 2) + 2 * (2 * I * (H // 128) * 2)  # 1,982,464 + 123,904
@@ -72,6 +73,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--skip-kernel-pass", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true",
+                    help="skip the prefill_8192 (Zipf routing) layer timing and its MFMA utilisation")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed region, copy a 512 MiB buffer 5 times (a kernel of known "
                          "traffic, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -347,6 +350,58 @@ def main() -> int:
             f"{ent_us + gum_us:.1f} us here)")
         del logits
 
+    # ---- prefill_8192: T = 8192, Zipf(1.1) expert popularity (not part of `value`)
+    # The same layer at prefill size, where the expert GEMMs are real
+    # contractions: 2 * 65536 routed rows * (2I*H + H*I) = 779.5 GFLOP.
+    prefill = None
+    if not args.skip_kernel_pass and not args.skip_prefill:
+        Tp = 8192
+        xp_, nwp, idsp, wp = wl.layer_inputs(Tp, 4, zipf_s=1.1)
+        xpg, nwpg, idspg, wpg = xp_.to(dev), nwp.to(dev), idsp.to(dev), wp.to(dev)
+        yp = torch.empty(Tp, H, dtype=torch.bfloat16, device=dev)
+        wsp = torch.empty(int(L.ksl_moe_workspace_bytes(Tp, TOPK, E, H, I)), dtype=torch.uint8, device=dev)
+        flops = 2.0 * Tp * TOPK * (2 * I * H + H * I)
+        counts = torch.bincount(idsp.reshape(-1), minlength=E)
+
+        def pstep(exp):
+            rc = L.ksl_moe_layer_forward(p(xpg), lib.DTYPE_BF16, H, p(nwpg), lib.DTYPE_BF16, 1e-6, p(idspg), p(wpg),
+                                         lib.DTYPE_F32, p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q),
+                                         p(exp.dn_s), p(exp.dn_z), lib.DN_LAYOUT_TILED, Tp, TOPK, E, H, I,
+                                         exp._ksl_act, p(yp), lib.DTYPE_BF16, H, p(wsp), wsp.numel(), st)
+            if rc:
+                lib.check(rc, "ksl_moe_layer_forward")
+
+        for i in range(3):
+            pstep(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        nrep = 10
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(nrep):
+            pstep(sets[i % len(sets)])
+        b.record()
+        torch.cuda.synchronize()
+        p_us = a.elapsed_time(b) * 1e3 / nrep
+        prunner = layer_mod.LayerRunner(Tp, TOPK, E, H, I, dev)
+        pev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(layer_mod.STAGES) + 1)] for _ in range(nrep)]
+        for i in range(nrep):
+            prunner.run(xpg, nwpg, 1e-6, sets[i % len(sets)], idspg, wpg, events=pev[i])
+        torch.cuda.synchronize()
+        pk = {name: sum(pev[i][k].elapsed_time(pev[i][k + 1]) for i in range(nrep)) * 1e3 / nrep
+              for k, name in enumerate(layer_mod.STAGES)}
+        tflops = flops / (p_us * 1e-6) / 1e12
+        gemm_us = pk["gateup"] + pk["down"]
+        prefill = {"tokens": Tp, "zipf_s": 1.1, "max_rows_per_expert": int(counts.max()),
+                   "min_rows_per_expert": int(counts.min()), "layer_us": round(p_us, 1),
+                   "gflop": round(flops / 1e9, 1), "layer_TFLOPs": round(tflops, 1),
+                   "mfma_utilisation": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                   "gemm_TFLOPs": round(flops / (gemm_us * 1e-6) / 1e12, 1),
+                   "kernels_us": {k: round(v, 1) for k, v in pk.items()}}
+        log(f"[bench] prefill_8192 (Zipf 1.1, rows/expert {int(counts.min())}..{int(counts.max())}): "
+            f"{p_us:.1f} us/layer, {tflops:.1f} TFLOP/s = {100 * tflops / MFMA_PEAK_TFLOPS:.1f}% of the "
+            f"2.5 PFLOP/s dense f16 MFMA peak; kernels " + ", ".join(f"{k} {v:.1f}" for k, v in pk.items()))
+        del xpg, yp, wsp, prunner
+
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
@@ -415,6 +470,7 @@ def main() -> int:
             "router_us": None if router_us is None else round(router_us, 3),
             "block_tail": tail,
             "sampler": sampler,
+            "prefill_8192": prefill,
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

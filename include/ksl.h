@@ -143,16 +143,20 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
  * a trailing 64-element group (I % 128 == 64) with offset c*16 + i*8 + j
  * stored at i*32 + c*8 + s(j). T: the tokens of a16 (T*topk routed rows;
  * with at least E of them the first weight groups are fetched before the
- * routing is read). */
+ * routing is read; above 8192 of them each workgroup takes a block of at most
+ * 128 rows of one expert). */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
                        int64_t T, int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
 
 /* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
- * out3 fp16 [T*topk, H] row per sorted slot, natural column order. dn_layout
- * as in ksl_moe_w4a16_forward. */
+ * out3 fp16 [T*topk, H] row per sorted slot, natural column order. nrows:
+ * the routed rows (T*topk), which size the grid (above 8192 routed rows each
+ * workgroup takes a block of at most 128 rows of one expert, so that a heavy
+ * expert spreads over many workgroups). dn_layout as in ksl_moe_w4a16_forward. */
 int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, int dn_layout, void* stream);
+                 const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,
+                 void* stream);
 
 /* Load-time repack of the down weights into the layout the down kernel loads
  * (the row f3 of the loader: the reference's precedent is the preshuffled

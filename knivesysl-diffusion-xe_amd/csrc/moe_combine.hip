@@ -19,7 +19,8 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
                   int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint);
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout);
+                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout,
+                int64_t nrows);
 
 namespace {
 
@@ -340,7 +341,7 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -375,7 +376,7 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -414,7 +415,7 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout);
+    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
     if (rc) return rc;
     return launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, x, x_stride, post2_w,
                                post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);

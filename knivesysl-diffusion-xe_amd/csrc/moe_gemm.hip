@@ -44,6 +44,8 @@ namespace ksl {
 namespace {
 
 constexpr int kXcds = 8;
+constexpr int kRowBlock = 128;       // rows per workgroup block of a large routing
+constexpr int kRowBlockFrom = 8192;  // routed rows above which experts split into row blocks
 
 // Index of the calling wave in its workgroup, in a scalar register (branches
 // on it are uniform).
@@ -54,6 +56,53 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     if (nblocks % kXcds != 0) return bid;
     return (bid % kXcds) * (nblocks / kXcds) + bid / kXcds;
+}
+
+// Row blocks (large routings): the rows of each expert split into blocks of at
+// most rb rows, numbered expert by expert (expert e has ceil(cnt_e / rb) of
+// them). The block `blk` of a workgroup is found by wave 0 from the offsets
+// (a wave scan of the per-expert block counts, 64 experts at a time) and
+// broadcast through LDS; every thread gets the same (e, start, M), M = 0
+// past the last block. One workgroup barrier, taken by every wave.
+__device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offsets, int E, int rb, int blk,
+                                               int& e, int& start, int& M) {
+    __shared__ int info[3];
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        if (lane == 0) {
+            info[0] = 0;
+            info[1] = 0;
+            info[2] = 0;
+        }
+        int base = 0;  // blocks of the experts before this batch
+        for (int e0 = 0; e0 < E; e0 += kWave) {
+            const int ex = e0 + lane;
+            int o0 = 0, cnt = 0;
+            if (ex < E) {
+                o0 = offsets[ex];
+                cnt = offsets[ex + 1] - o0;
+            }
+            const int nb = (cnt + rb - 1) / rb;
+            int incl = nb;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const int o = __shfl_up(incl, off, kWave);
+                if (lane >= off) incl += o;
+            }
+            const int excl = base + incl - nb;
+            if (ex < E && blk >= excl && blk < excl + nb) {
+                const int b = blk - excl;
+                info[0] = ex;
+                info[1] = o0 + b * rb;
+                info[2] = cnt - b * rb < rb ? cnt - b * rb : rb;
+            }
+            base += __shfl(incl, kWave - 1, kWave);
+        }
+    }
+    __syncthreads();
+    e = info[0];
+    start = info[1];
+    M = info[2];
 }
 
 
@@ -150,6 +199,8 @@ struct GuArgs {
     f16* out2;
     int topk, I, H;
     int early;  // producers issue the first weight groups before reading the routing
+    int E;
+    int rb;     // > 0: one workgroup per (block of rb rows of an expert, column block)
 };
 
 template <int NC, int NP, int R>
@@ -338,14 +389,21 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int e = tile / nb_per_e;
-    const int c0 = (tile - e * nb_per_e) * S::kCols;
-    if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R>(A, e, c0, lds);
-    const int start = A.offsets[e];
-    const int M = A.offsets[e + 1] - start;
-    if (M <= 0) {
-        vm_wait<0>();  // early weight loads land before the workgroup's LDS is released
-        return;
+    const int unit = tile / nb_per_e;  // expert, or row block when A.rb > 0
+    const int c0 = (tile - unit * nb_per_e) * S::kCols;
+    int e, start, M;
+    if (A.rb > 0) {
+        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
+        if (M <= 0) return;  // past the last row block (uniform)
+    } else {
+        e = unit;
+        if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R>(A, e, c0, lds);
+        start = A.offsets[e];
+        M = A.offsets[e + 1] - start;
+        if (M <= 0) {
+            vm_wait<0>();  // early weight loads land before the workgroup's LDS is released
+            return;
+        }
     }
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
@@ -422,9 +480,12 @@ int device_cus() {
 }
 
 template <int NC, int NP, int R>
-int launch_gateup_nc(const GuArgs& A, int64_t E, int act, hipStream_t st) {
+int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStream_t st) {
     using S = GuShape<NC, NP, R>;
-    const unsigned grid = static_cast<unsigned>(E * (A.I / S::kCols));
+    // row blocks: at most ceil(nrows / rb) + E of them (one partial block per expert)
+    const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
+    if (units * (A.I / S::kCols) >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    const unsigned grid = static_cast<unsigned>(units * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
     if (lds > kLdsBytes) return KSL_ERR_SHAPE;
     static const bool attr_set = set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>)) &&
@@ -482,6 +543,8 @@ struct DnArgs {
     const f16* dn_z;
     f16* out3;
     int H, I, nsplit, tpw;  // tpw: 16-column tiles per workgroup
+    int E;
+    int rb;                 // > 0: one workgroup per (block of rb rows of an expert, column split)
 };
 
 // LDS: activation blocks [kMaxMt][2G] (1 KB each, frag_pos order), then the
@@ -667,10 +730,16 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int e = bid / A.nsplit;
-    const int h = bid - e * A.nsplit;
-    const int start = A.offsets[e];
-    const int M = A.offsets[e + 1] - start;
+    const int unit = bid / A.nsplit;  // expert, or row block when A.rb > 0
+    const int h = bid - unit * A.nsplit;
+    int e, start, M;
+    if (A.rb > 0) {
+        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
+    } else {
+        e = unit;
+        start = A.offsets[e];
+        M = A.offsets[e + 1] - start;
+    }
     const int col0 = h * A.tpw * 16;
     const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
     if (M <= 0 || ncols <= 0) return;
@@ -913,10 +982,16 @@ __global__ __launch_bounds__(kDdWaves * kWave) void down_dma_kernel(DnArgs A) {
     __shared__ __attribute__((aligned(16))) char slots0[kDdWaves][C::kSlot];
     __shared__ __attribute__((aligned(16))) char slots1[kDdWaves][C::kSlot];
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int e = bid / A.nsplit;
-    const int h = bid - e * A.nsplit;
-    const int start = A.offsets[e];
-    const int M = A.offsets[e + 1] - start;
+    const int unit = bid / A.nsplit;  // expert, or row block when A.rb > 0
+    const int h = bid - unit * A.nsplit;
+    int e, start, M;
+    if (A.rb > 0) {
+        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
+    } else {
+        e = unit;
+        start = A.offsets[e];
+        M = A.offsets[e + 1] - start;
+    }
     const int col0 = h * A.tpw * 16;
     const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
     if (M <= 0 || ncols <= 0) return;
@@ -989,18 +1064,24 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // with at least as many routed rows as experts most experts have rows: the
     // first weight groups go out before the routing is read
     A.early = nrows_hint >= E ? 1 : 0;
+    A.E = static_cast<int>(E);
+    // large routings: experts split into row blocks, so that a heavy expert
+    // (thousands of rows at prefill) spreads over many workgroups
+    A.rb = nrows_hint > kRowBlockFrom ? kRowBlock : 0;
+    if (A.rb > 0) A.early = 0;
     // widest column block that divides I: 176 (11 consumers), 128, or 64
     // (ring depth 4 where the LDS holds it: 176 columns up to H = 3712)
     if (I % 176 == 0) {
-        if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, act, st);
-        return launch_gateup_nc<11, 5, 3>(A, E, act, st);
+        if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, nrows_hint, act, st);
+        return launch_gateup_nc<11, 5, 3>(A, E, nrows_hint, act, st);
     }
-    if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, act, st);
-    return launch_gateup_nc<4, 4, 4>(A, E, act, st);
+    if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, nrows_hint, act, st);
+    return launch_gateup_nc<4, 4, 4>(A, E, nrows_hint, act, st);
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
-                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout) {
+                const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout,
+                int64_t nrows) {
     if (!out2 || !offsets || !dn_q || !dn_s || !dn_z || !out3) return KSL_ERR_ARG;
     if (layout != kDnRef && layout != kDnTiled) return KSL_ERR_ARG;
     if (E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
@@ -1018,6 +1099,9 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     A.out3 = static_cast<f16*>(out3);
     A.H = static_cast<int>(H);
     A.I = static_cast<int>(I);
+    A.E = static_cast<int>(E);
+    A.rb = nrows > kRowBlockFrom ? kRowBlock : 0;
+    const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
     const int G = static_cast<int>(I / 64);
     // columns per workgroup: enough workgroups to fill the CUs, few enough
     // columns that their scale / zero rows fit in LDS beside the activations
@@ -1029,10 +1113,10 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     nsplit = (te + tpw - 1) / tpw;
     A.tpw = static_cast<int>(tpw);
     A.nsplit = static_cast<int>(nsplit);
-    const int64_t grid = E * nsplit;
+    const int64_t grid = units * nsplit;
     if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const size_t lds = dn_lds_bytes(G, static_cast<int>(tpw * 16));
-    if (kDownDmaTiles && layout == kDnRef && G <= 12) {
+    if (kDownDmaTiles && layout == kDnRef && A.rb == 0 && G <= 12) {
         // per-wave DMA tiles (static LDS, 8 waves): its own split, same rule
         int64_t ns = std::max<int64_t>(1, std::min<int64_t>((device_cus() + E - 1) / E, te));
         const int64_t tp = (te + ns - 1) / ns;
@@ -1071,9 +1155,10 @@ extern "C" int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, c
 
 extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q,
                             const void* dn_s, const void* dn_z, int64_t E, int64_t H, int64_t I,
-                            void* out3, int dn_layout, void* stream) {
+                            int64_t nrows, void* out3, int dn_layout, void* stream) {
+    if (nrows < 0) return KSL_ERR_SHAPE;
     return ksl::launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3,
-                            static_cast<hipStream_t>(stream), dn_layout);
+                            static_cast<hipStream_t>(stream), dn_layout, nrows);
 }
 
 extern "C" int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled,

@@ -113,7 +113,7 @@ class LayerRunner:
         if ev:
             ev[2].record()
         rc = L.ksl_moe_down(p(self.out2), p(self.offsets), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z), E, H, I,
-                            p(self.out3), dn_layout(exp), st)
+                            T * tk, p(self.out3), dn_layout(exp), st)
         _lib.check(rc, "ksl_moe_down")
         if ev:
             ev[3].record()

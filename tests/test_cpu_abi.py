@@ -73,9 +73,10 @@ def test_validation_returns_before_device_work(L):
     assert L.ksl_moe_gateup_act(P((1 << 20) + 8), fake, fake, 256, 8, fake, fake, fake, 128, 2816, 704, 1, fake,
                                 null) == 3
     # down: I not a multiple of 64, I above 1024
-    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, fake, 0, null) == 2
-    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, fake, 0, null) == 2
-    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, fake, 7, null) == 1   # unknown layout
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 700, 2048, fake, 0, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, 2048, fake, 0, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, fake, 7, null) == 1   # unknown layout
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, -1, fake, 0, null) == 2
     # repack: shapes, in-place refused, alignment
     assert L.ksl_moe_repack_down(fake, 128, 2816, 700, P((1 << 21)), null) == 2
     assert L.ksl_moe_repack_down(fake, 128, 2816, 704, fake, null) == 1

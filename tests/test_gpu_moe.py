@@ -194,7 +194,7 @@ def _stage_run(gpu, exp, hidden, ids, act):
                               lib.ptr(exp.gu_z), E, H, I, act, lib.ptr(out2), st)
     lib.check(rc, "ksl_moe_gateup_act")
     rc = L.ksl_moe_down(lib.ptr(out2), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
-                        E, H, I, lib.ptr(out3), lib.DN_LAYOUT_REF, st)
+                        E, H, I, T * tk, lib.ptr(out3), lib.DN_LAYOUT_REF, st)
     lib.check(rc, "ksl_moe_down")
     torch.cuda.synchronize()
     return sr, off, inv, out2, out3
@@ -412,3 +412,37 @@ def test_tiled_down_forward_is_bit_identical(gpu, T, tk, E, H, I, seed):
     assert a.dn_q.data_ptr() == b.dn_q.data_ptr() and a.dn_tiled and b.dn_tiled
     assert torch.equal(a.dn_q, exp_t.dn_q)
     assert pe.repack_experts(model, verbose=False) == 2 and a.dn_q.data_ptr() == b.dn_q.data_ptr()  # idempotent
+
+
+@pytest.mark.parametrize("T,tk,E,H,I,zipf,seed", [(1200, 8, 16, 256, 128, None, 91), (2048, 8, 128, 512, 256, 1.1, 92)])
+def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
+    """Above 8192 routed rows gate/up and down give each workgroup a block of
+    at most 128 rows of one expert; the rows' values do not depend on the
+    split: gate/up and down outputs equal the one-workgroup-per-expert mode
+    (selected here by a small row count) bit for bit."""
+    lib = load_pkg()._lib
+    wl = load_mod("workloads")
+    L = lib.load()
+    ids, _ = wl.make_routing(T, E, tk, seed, zipf)
+    hidden = wl.make_hidden(T, H, seed + 1)
+    exp = wl.make_experts(E, H, I, seed + 2, device=gpu)
+    idsg = ids.to(gpu)
+    sr, off, inv, a16 = _route(gpu, idsg, hidden.to(gpu), E)
+    counts = torch.bincount(ids.reshape(-1), minlength=E)
+    print(f"row blocks T={T} E={E} rows/expert {int(counts.min())}..{int(counts.max())}", flush=True)
+    st = lib.stream_of(a16)
+    outs2, outs3 = [], []
+    for t_hint, nrows in ((T, T * tk), (1, 100)):   # row blocks, then one workgroup per expert
+        out2 = torch.empty(T * tk, I, dtype=torch.float16, device=gpu)
+        out3 = torch.empty(T * tk, H, dtype=torch.float16, device=gpu)
+        rc = L.ksl_moe_gateup_act(lib.ptr(a16), lib.ptr(sr), lib.ptr(off), t_hint, tk, lib.ptr(exp.gu_q),
+                                  lib.ptr(exp.gu_s), lib.ptr(exp.gu_z), E, H, I, lib.ACT_SILU, lib.ptr(out2), st)
+        lib.check(rc, "ksl_moe_gateup_act")
+        rc = L.ksl_moe_down(lib.ptr(out2), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
+                            E, H, I, nrows, lib.ptr(out3), lib.DN_LAYOUT_REF, st)
+        lib.check(rc, "ksl_moe_down")
+        outs2.append(out2)
+        outs3.append(out3)
+    torch.cuda.synchronize()
+    assert torch.equal(outs2[0].view(torch.int16), outs2[1].view(torch.int16))
+    assert torch.equal(outs3[0].view(torch.int16), outs3[1].view(torch.int16))
