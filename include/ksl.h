@@ -150,7 +150,8 @@ int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
 
 /* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
- * out3 fp16 [T*topk, H] row per sorted slot, natural column order. nrows:
+ * out3 fp16 [T*topk, H] row per sorted slot, natural column order, 8-byte
+ * aligned (written 4 columns per store). nrows:
  * the routed rows (T*topk), which size the grid (above 8192 routed rows each
  * workgroup takes a block of at most 128 rows of one expert, so that a heavy
  * expert spreads over many workgroups). dn_layout as in ksl_moe_w4a16_forward. */
@@ -159,8 +160,8 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
                  void* stream);
 
 /* Load-time repack of the down weights into the layout the down kernel loads
- * (the row f3 of the loader: the reference's precedent is the preshuffled
- * down pack, kernels/fused_moe_w4_v2.py:187-206). Out of place, same size as
+ * (the reference's precedent is the preshuffled down pack,
+ * kernels/fused_moe_w4_v2.py:187-206). Out of place, same size as
  * dn_q [E, H, I/2]. Within each 16-row tile (base address unchanged): unit u
  * < I/128 is 1 KB, 16 bytes per lane l = c*16 + col: row col, bytes
  * u*64 + c*16 .. +16; then for I % 128 == 64 a 512-byte tail, 8 bytes per

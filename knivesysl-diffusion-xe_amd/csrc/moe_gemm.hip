@@ -619,7 +619,7 @@ __device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[kMa
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + g2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(a, b, acc[t]);
+                acc[t] = mfma16x16x32(b, a, acc[t]);
             }
         }
         // one 128-K block at a time: the other waves hide its LDS latency, and
@@ -637,7 +637,7 @@ __device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[kMa
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + G2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(a, b, acc[t]);
+                acc[t] = mfma16x16x32(b, a, acc[t]);
             }
         }
     }
@@ -673,10 +673,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* p, uint32_t byt
 }
 constexpr uint32_t kDropOffset = 0x80000000u;
 
-// One tile: MT M tiles x 16 columns. The stores have no branches (rows past
-// the chunk, or a repeated tile, take an out-of-range offset), so every wave
-// issues the same number of memory operations per tile and the waits on the
-// prefetched weights are exact.
+// One tile: MT M tiles x 16 columns. The weights are the MFMA's A operand and
+// the activations its B operand, so the accumulator is the tile transposed:
+// lane (col, c) holds row col of the M tile, output columns 4c .. 4c+3, and
+// writes them with one 8-byte store (out3 is 8-byte aligned, H % 64 == 0).
+// The stores have no branches (rows past the chunk, or a
+// repeated tile, take an out-of-range offset), so every wave issues the same
+// number of memory operations per tile and the waits on the prefetched
+// weights are exact.
 template <int G2, bool TAIL, int MT>
 __device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a_lds, const f16* s_lds,
                                            const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int tile,
@@ -689,28 +693,27 @@ __device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a
     const int rl = tile * 16 + col;  // row of dn within the workgroup's columns
     dn_tile<G2, TAIL, MT>(w, acc, a_lds, s_lds + rl * G, z_lds + rl * G, c, fo, kn);
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int row = t * 16 + 4 * c + q;
-            const uint32_t off = valid && row < mrows ? static_cast<uint32_t>((row * H + colw + tile * 16 + col) * 2)
-                                                      : kDropOffset;
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16>(acc[t][q])),
-                                                  out, off, 0, 0);
-        }
+    for (int t = 0; t < MT; ++t) {
+        const int row = t * 16 + col;
+        const uint32_t off = valid && row < mrows ? static_cast<uint32_t>((row * H + colw + tile * 16 + 4 * c) * 2)
+                                                  : kDropOffset;
+        const f16x4 v{static_cast<f16>(acc[t][0]), static_cast<f16>(acc[t][1]), static_cast<f16>(acc[t][2]),
+                      static_cast<f16>(acc[t][3])};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), out, off, 0, 0);
+    }
 }
 
 // A wave's tiles of one chunk: tiles wave + k*kDnWaves, k < nmine, weights of
 // tile k+1 loaded while tile k is computed. Loads are unconditional (past the
 // last tile they repeat it: an L2 hit), a repeated tile's stores are dropped,
 // so between a buffer's loads and its use exactly the other buffer's loads and
-// one tile's 4*MT stores are issued (on entry w0 has landed already).
+// one tile's MT stores are issued (on entry w0 has landed already).
 template <int G2, bool TAIL, int MT, int LAYOUT>
 __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, const uint8_t* wrow, int rb,
                                          int nmine, int wave, const char* a_lds, const f16* s_lds,
                                          const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int colw, int mrows,
                                          int col, int c, int fo, const NibConsts& kn) {
-    constexpr int kAfter = G2 + (TAIL ? 1 : 0) + 4 * MT;
+    constexpr int kAfter = G2 + (TAIL ? 1 : 0) + MT;
     for (int k = 0; k < nmine; k += 2) {
         const int k1 = k + 1 < nmine ? k + 1 : nmine - 1;
         const int k2 = k + 2 < nmine ? k + 2 : nmine - 1;
@@ -831,213 +834,6 @@ __global__ __launch_bounds__(256) void repack_down_kernel(const uint8_t* __restr
     }
 }
 
-// ------------------------------------------------------ down, per-wave DMA
-// The variant used while its LDS fits (I <= 768). Like the register-streamed
-// kernel, a workgroup owns one expert and a range of 16-column tiles, with
-// the chunk's activations in LDS; but each wave fetches its next tile itself
-// as one contiguous piece (16 rows x I/2 bytes of dn_q, plus the tile's 16
-// s rows and 16 z rows) by direct global->LDS loads into the free one of its
-// two private LDS slots, and reads the B operands from LDS. A contiguous
-// fetch streams at a higher rate than the 16-rows-per-load register pattern,
-// and no register buffers are needed. The loads are issued as asm (with M0
-// saved and restored): the compiler then adds no waits of its own for them,
-// the waits are explicit (vm_wait) and count exactly the tile's loads and the
-// previous tile's stores; nothing else in the kernel touches vmcnt.
-constexpr int kDdWaves = 8;
-// Off: with one tile of prefetch per wave (the LDS holds no more) it streams
-// no faster than the register-streamed kernel (41.5 vs 40 us at the
-// 256-token layer); kept for its contiguous-fetch path.
-constexpr bool kDownDmaTiles = false;
-
-template <int G2, bool TAIL>
-struct DdCfg {
-    static constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-    static constexpr int kRb = 32 * G;                  // bytes per dn row
-    static constexpr int kTileW = 16 * kRb;             // weight bytes of a tile
-    static constexpr int kTileS = 16 * G * 2;           // s (and z) bytes of a tile
-    static constexpr int kSlot = kTileW + 2 * kTileS;
-    static constexpr int kA = kMaxMt * 2 * G * kBlk;
-    static constexpr int kWDma = (kTileW + 1023) / 1024;
-    static constexpr int kDma = kWDma + 1;              // weights, then s and z in one load
-    static constexpr size_t kLds = static_cast<size_t>(kA) + 2 * kDdWaves * kSlot;
-    static_assert(2 * kTileS <= 1024, "s and z of a tile in one load");
-};
-
-// Direct global -> LDS copy of one fragment block (lane L's 16 bytes at
-// lds_block + 16*L), as asm: M0 holds the LDS address during the load only.
-__device__ __forceinline__ void dma16_asm(const void* src, const char* lds_block) {
-    const auto lp = (__attribute__((address_space(3))) const char*)lds_block;
-    const uint32_t m = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lp)));
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(src), "s"(m)
-                 : "memory");
-}
-
-// Tile `tile` (row r0 of dn) into `slot`: C::kDma loads, every one with lane 0 active.
-template <int G2, bool TAIL>
-__device__ __forceinline__ void dd_issue(const DnArgs& A, int64_t r0, char* slot, int lane) {
-    using C = DdCfg<G2, TAIL>;
-    constexpr int G = C::G;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of the slot are done
-    const char* w = reinterpret_cast<const char*>(A.dn_q) + r0 * C::kRb;
-#pragma unroll
-    for (int j = 0; j < C::kWDma; ++j) {
-        const int off = j * 1024 + lane * 16;
-        if (j < C::kWDma - 1 || off < C::kTileW) dma16_asm(w + off, slot + j * 1024);
-    }
-    constexpr int kSq = C::kTileS / 16;  // 16-byte chunks of s (and of z)
-    if (lane < 2 * kSq) {
-        const char* src = lane < kSq ? reinterpret_cast<const char*>(A.dn_s + r0 * G) + lane * 16
-                                     : reinterpret_cast<const char*>(A.dn_z + r0 * G) + (lane - kSq) * 16;
-        dma16_asm(src, slot + C::kTileW);
-    }
-}
-
-template <int G2, bool TAIL, int MT>
-__device__ __forceinline__ void dd_do_tile(const char* __restrict__ slot, const char* __restrict__ a_lds,
-                                           __amdgpu_buffer_rsrc_t out, int H, int colt, bool valid, int mrows,
-                                           int col, int c, int fo, const NibConsts& kn) {
-    using C = DdCfg<G2, TAIL>;
-    constexpr int G = C::G;
-    const f16* srow = reinterpret_cast<const f16*>(slot + C::kTileW) + col * G;
-    const f16* zrow = srow + 16 * G;
-    const char* wrow = slot + col * C::kRb;
-    f32x4 acc[kMaxMt];
-#pragma unroll
-    for (int t = 0; t < kMaxMt; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int g2 = 0; g2 < G2; ++g2) {
-        const int grp = 2 * g2 + (c >> 1);
-        const f16 sv = srow[grp];
-        const ZeroPair zc = zero_pair(zrow[grp]);
-        const u32x4 wq = *reinterpret_cast<const u32x4*>(wrow + g2 * 64 + c * 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f16x8 b = nib8_dequant(wq[i], zc, f16x2{sv, sv}, kn);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + g2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(a, b, acc[t]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (TAIL) {
-        const f16 sv = srow[2 * G2];
-        const ZeroPair zc = zero_pair(zrow[2 * G2]);
-        const u32x2 wt = *reinterpret_cast<const u32x2*>(wrow + G2 * 64 + c * 8);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const f16x8 b = nib8_dequant(wt[i], zc, f16x2{sv, sv}, kn);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + G2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(a, b, acc[t]);
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int row = t * 16 + 4 * c + q;
-            const uint32_t off = valid && row < mrows ? static_cast<uint32_t>((row * H + colt + col) * 2) : kDropOffset;
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16>(acc[t][q])),
-                                                  out, off, 0, 0);
-        }
-}
-
-// A wave's tiles of one chunk (tiles wave + k*kDdWaves, k < nmine); on entry
-// tile 0 is in slot0 and has landed. Issues are unconditional (past the last
-// tile they repeat it), a repeated tile's stores are dropped, so each wait
-// allows exactly the other slot's C::kDma loads and one tile's 4*MT stores.
-template <int G2, bool TAIL, int MT>
-__device__ __forceinline__ void dd_tiles(const DnArgs& A, char* slot0, char* slot1, const char* a_lds,
-                                         __amdgpu_buffer_rsrc_t out, int64_t wrow0, int colw, int nmine, int wave,
-                                         int mrows, int lane, int col, int c, int fo, const NibConsts& kn) {
-    using C = DdCfg<G2, TAIL>;
-    constexpr int kAfter = C::kDma + 4 * MT;
-    for (int k = 0; k < nmine; k += 2) {
-        const int k1 = k + 1 < nmine ? k + 1 : nmine - 1;
-        const int k2 = k + 2 < nmine ? k + 2 : nmine - 1;
-        const int t0 = wave + k * kDdWaves, t1 = wave + k1 * kDdWaves, t2 = wave + k2 * kDdWaves;
-        dd_issue<G2, TAIL>(A, wrow0 + t1 * 16, slot1, lane);
-        vm_wait<kAfter>();
-        asm volatile("" ::: "memory");
-        dd_do_tile<G2, TAIL, MT>(slot0, a_lds, out, A.H, colw + t0 * 16, true, mrows, col, c, fo, kn);
-        dd_issue<G2, TAIL>(A, wrow0 + t2 * 16, slot0, lane);
-        vm_wait<kAfter>();
-        asm volatile("" ::: "memory");
-        dd_do_tile<G2, TAIL, MT>(slot1, a_lds, out, A.H, colw + t1 * 16, k + 1 < nmine, mrows, col, c, fo, kn);
-    }
-}
-
-template <int G2, bool TAIL>
-__global__ __launch_bounds__(kDdWaves * kWave) void down_dma_kernel(DnArgs A) {
-    using C = DdCfg<G2, TAIL>;
-    constexpr int G = C::G;
-    __shared__ __attribute__((aligned(16))) char a_lds[C::kA];
-    __shared__ __attribute__((aligned(16))) char slots0[kDdWaves][C::kSlot];
-    __shared__ __attribute__((aligned(16))) char slots1[kDdWaves][C::kSlot];
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int unit = bid / A.nsplit;  // expert, or row block when A.rb > 0
-    const int h = bid - unit * A.nsplit;
-    int e, start, M;
-    if (A.rb > 0) {
-        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
-    } else {
-        e = unit;
-        start = A.offsets[e];
-        M = A.offsets[e + 1] - start;
-    }
-    const int col0 = h * A.tpw * 16;
-    const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
-    if (M <= 0 || ncols <= 0) return;
-    const int ntiles = ncols >> 4;
-    const int wave = wave_id();
-    const int lane = threadIdx.x & (kWave - 1);
-    const int col = lane & 15, c = lane >> 4;
-    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
-    const int fo = frag_pos(col, c) * 16;
-    const NibConsts kn = nib_consts();
-    const int64_t wrow0 = static_cast<int64_t>(e) * A.H + col0;  // first dn row of the workgroup
-    const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDdWaves + 1 : 0;
-    char* slot0 = slots0[wave];
-    char* slot1 = slots1[wave];
-    for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
-        const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
-        const int mt = mrows > 16 ? 2 : 1;
-        if (m0 > 0) lds_sync();  // every wave is done with the previous chunk's activations
-        // activation blocks, as in dn_stage_a
-        for (int b = wave; b < mt * 2 * G; b += kDdWaves) {
-            const int t = b / (2 * G), bb = b - t * 2 * G;
-            const int off = bb < 4 * G2 ? (bb >> 2) * 128 + (bb & 3) * 32 : G2 * 128 + (bb - 4 * G2) * 32;
-            int r = t * 16 + rr;
-            if (r >= mrows) r = mrows - 1;
-            dma16_asm(A.out2 + static_cast<int64_t>(start + m0 + r) * A.I + off + ch * 8, a_lds + b * kBlk);
-        }
-        if (nmine > 0) dd_issue<G2, TAIL>(A, wrow0 + wave * 16, slot0, lane);
-        vm_wait<0>();
-        dma_barrier();
-        const __amdgpu_buffer_rsrc_t out =
-            raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
-        if (mt == 2)
-            dd_tiles<G2, TAIL, 2>(A, slot0, slot1, a_lds, out, wrow0, col0, nmine, wave, mrows, lane, col, c, fo, kn);
-        else
-            dd_tiles<G2, TAIL, 1>(A, slot0, slot1, a_lds, out, wrow0, col0, nmine, wave, mrows, lane, col, c, fo, kn);
-    }
-    vm_wait<0>();  // the last (repeated) tile load lands before the LDS is released
-}
-
-template <int G2, bool TAIL>
-int launch_down_dma(const DnArgs& A, unsigned grid, hipStream_t st) {
-    hipLaunchKernelGGL((down_dma_kernel<G2, TAIL>), dim3(grid), dim3(kDdWaves * kWave), 0, st, A);
-    KSL_LAUNCH_CHECK();
-    return KSL_OK;
-}
-
 }  // namespace
 
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
@@ -1088,7 +884,7 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     if (H % 64 != 0 || I % 64 != 0 || I > 64 * kDnMaxG || H >= (1 << 24) || E >= (1 << 24)) return KSL_ERR_SHAPE;
     if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(out2) % 16 ||
         reinterpret_cast<uintptr_t>(dn_s) % 16 || reinterpret_cast<uintptr_t>(dn_z) % 16 ||
-        reinterpret_cast<uintptr_t>(out3) % 2)
+        reinterpret_cast<uintptr_t>(out3) % 8)
         return KSL_ERR_ALIGN;
     DnArgs A;
     A.out2 = static_cast<const f16*>(out2);
@@ -1116,23 +912,6 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     const int64_t grid = units * nsplit;
     if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const size_t lds = dn_lds_bytes(G, static_cast<int>(tpw * 16));
-    if (kDownDmaTiles && layout == kDnRef && A.rb == 0 && G <= 12) {
-        // per-wave DMA tiles (static LDS, 8 waves): its own split, same rule
-        int64_t ns = std::max<int64_t>(1, std::min<int64_t>((device_cus() + E - 1) / E, te));
-        const int64_t tp = (te + ns - 1) / ns;
-        ns = (te + tp - 1) / tp;
-        A.tpw = static_cast<int>(tp);
-        A.nsplit = static_cast<int>(ns);
-        const unsigned g = static_cast<unsigned>(E * ns);
-        switch (G) {
-#define KSL_DD_CASE(GG) \
-    case GG: return launch_down_dma<GG / 2, (GG % 2) != 0>(A, g, st);
-            KSL_DD_CASE(1) KSL_DD_CASE(2) KSL_DD_CASE(3) KSL_DD_CASE(4) KSL_DD_CASE(5) KSL_DD_CASE(6)
-            KSL_DD_CASE(7) KSL_DD_CASE(8) KSL_DD_CASE(9) KSL_DD_CASE(10) KSL_DD_CASE(11) KSL_DD_CASE(12)
-#undef KSL_DD_CASE
-            default: break;
-        }
-    }
     switch (G) {
 #define KSL_DN_CASE(GG) \
     case GG: return launch_down_g<GG / 2, (GG % 2) != 0>(A, static_cast<unsigned>(grid), lds, layout, st);

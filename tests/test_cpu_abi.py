@@ -77,6 +77,7 @@ def test_validation_returns_before_device_work(L):
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 1088, 2048, fake, 0, null) == 2
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, fake, 7, null) == 1   # unknown layout
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, -1, fake, 0, null) == 2
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, P((1 << 20) + 4), 0, null) == 3  # out3 % 8
     # repack: shapes, in-place refused, alignment
     assert L.ksl_moe_repack_down(fake, 128, 2816, 700, P((1 << 21)), null) == 2
     assert L.ksl_moe_repack_down(fake, 128, 2816, 704, fake, null) == 1
