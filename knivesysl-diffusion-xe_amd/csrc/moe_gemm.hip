@@ -19,21 +19,22 @@
 // the fp16 rounding of the dequantised weight.)
 //
 // Memory pipeline. Loads retire in issue order (one vmcnt counter per wave),
-// so a load consumed soon after issue would drain every weight prefetch behind
-// it. Only weight loads therefore go through registers in the steady state:
+// so a load consumed soon after issue would drain every prefetch behind it:
 //   - scales and zero-points of the workgroup's rows are copied to LDS once;
 //   - activations are copied to LDS in MFMA fragment order (each lane's 16
 //     bytes contiguous across the wave: conflict-free ds_read_b128);
-//   - gate/up streams K in slabs of two groups through a double-buffered LDS
-//     slab; the loads of slab s+1 are issued before the weight prefetches of
-//     slab s, so waiting for them never waits for those prefetches;
-//   - down holds all of its weights in registers (K = I is short) and reuses
-//     them for every 32-row chunk of its expert.
+//   - gate/up: producer waves stream weight and activation fragments of one
+//     128-K group per slot into an LDS ring by direct global -> LDS loads,
+//     consumer waves only read LDS (one barrier per group);
+//   - down: each wave streams its 16-column weight tiles through two register
+//     buffers with explicit vmcnt waits.
 //
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
-// rows (one or two 16-row M tiles). Workgroups are remapped so that all column
-// blocks of an expert run on the same XCD (shared L2 for its activations).
+// rows (one or two 16-row M tiles); above 8192 routed rows one workgroup per
+// block of at most 128 rows of an expert. Workgroups are remapped so that all
+// column blocks of an expert run on the same XCD (shared L2 for its
+// activations).
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
