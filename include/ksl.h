@@ -72,10 +72,14 @@ int ksl_rmsnorm(const void* x, int x_dtype, const void* w, int w_dtype, void* y,
 int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
                   int64_t* sorted_rows, int64_t* expert_ids, int64_t* inv, void* stream);
 
-/* Workspace bytes the fused forward needs for these shapes. */
+/* Workspace bytes the fused forward needs for these shapes: the routing
+ * (sorted rows, offsets, inv), the fp16 activations, out2, out3 and the
+ * per-block expert counts of the multi-block routing used above 4096 routed
+ * rows. */
 size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I);
 
-/* The whole W4A16 MoE forward, four launches, no host sync.
+/* The whole W4A16 MoE forward, four launches (five above 4096 routed rows:
+ * the routing then counts and places in two), no host sync.
  * Replaces fused_moe_w4_v2 (kernels/fused_moe_w4_v2.py:319-371):
  *   align -> gate/up + activation -> down -> fixed-order top-k combine.
  * hidden: [T, H] (bf16/fp16/fp32) with row stride hidden_stride;
@@ -113,13 +117,20 @@ int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const vo
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                           int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
 
-/* The first launch of ksl_moe_layer_forward: compact routing (as
+/* The first stage of ksl_moe_layer_forward: compact routing (as
  * ksl_moe_route) plus a16 = fp16(bf16(rmsnorm(x) [* norm_w])) in the gate/up
- * activation order, one launch. */
+ * activation order. One launch; above 4096 routed rows, when `scratch` holds
+ * ksl_moe_route_scratch_bytes(T, topk, E) bytes (4-byte aligned), two
+ * launches over many workgroups (per-block counts in scratch, then the stable
+ * placement; same results), else one routing workgroup. scratch may be NULL. */
 int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
                         int32_t* sorted_rows, int32_t* offsets, int32_t* inv, const void* x, int x_dtype,
                         int64_t x_stride, const void* norm_w, int norm_w_dtype, float eps, int64_t H,
-                        void* a16, void* stream);
+                        void* a16, void* scratch, size_t scratch_bytes, void* stream);
+
+/* Scratch bytes of the multi-block routing: ceil(T*topk / 4096) * E int32
+ * block counts (0 when T*topk <= 4096). Not a reference entry point. */
+size_t ksl_moe_route_scratch_bytes(int64_t T, int64_t topk, int64_t E);
 
 /* ---- the forward's stages, exposed for tests and for callers that fuse
  *      their own pipeline (same kernels as ksl_moe_w4a16_forward) ---------- */

@@ -45,7 +45,8 @@ SIGNATURES = {
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
-    "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P], _I),
+    "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P, _SZ, _P], _I),
+    "ksl_moe_route_scratch_bytes": ([_I64, _I64, _I64], _SZ),
     "ksl_moe_router": ([_P, _I, _I64, _P, _P, _P, _I, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_combine_post": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _P, _F,
                               _P, _I, _P, _I64, _P], _I),

@@ -9,12 +9,14 @@
 
 namespace ksl {
 
+// bcnt: workspace for the per-block counts of the multi-block routing
+// (ceil(T*topk / 4096) * E int32), or null for the single-workgroup routing.
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
-                  int64_t H, void* a16, hipStream_t st);
+                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st);
 int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
-               int wd, float eps, int64_t H, void* a16, hipStream_t st);
+               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st);
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
                   int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint);
@@ -266,9 +268,10 @@ int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int
 
 // Workspace layout of the fused forward (each region 256-byte aligned):
 //   sorted_rows i32[Nexp] | offsets i32[E+1] | inv i32[Nexp] |
-//   a16 f16[T*H] | out2 f16[Nexp*I] | out3 f16[Nexp*H]
+//   a16 f16[T*H] | out2 f16[Nexp*I] | out3 f16[Nexp*H] |
+//   bcnt i32[ceil(Nexp/4096) * E] (per-block expert counts of the multi-block routing)
 struct MoeWorkspace {
-    size_t sorted_rows, offsets, inv, a16, out2, out3, total;
+    size_t sorted_rows, offsets, inv, a16, out2, out3, bcnt, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -283,6 +286,7 @@ static MoeWorkspace moe_workspace_layout(int64_t T, int64_t topk, int64_t E, int
     w.a16 = off;         off += align256(static_cast<size_t>(T * H) * 2);
     w.out2 = off;        off += align256(nexp * static_cast<size_t>(I) * 2);
     w.out3 = off;        off += align256(nexp * static_cast<size_t>(H) * 2);
+    w.bcnt = off;        off += align256((nexp + 4095) / 4096 * static_cast<size_t>(E) * 4);
     w.total = off;
     return w;
 }
@@ -335,9 +339,10 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     void* a16 = ws + L.a16;
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
+    int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
     hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
-                           hidden_stride, H, a16, st);
+                           hidden_stride, H, a16, bcnt, st);
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
@@ -370,9 +375,10 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     void* a16 = ws + L.a16;
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
+    int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
     hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
-                        norm_w_dtype, eps, H, a16, st);
+                        norm_w_dtype, eps, H, a16, bcnt, st);
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
@@ -409,9 +415,10 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
     void* a16 = ws + L.a16;
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
+    int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
     hipStream_t st = static_cast<hipStream_t>(stream);
     rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, KSL_DTYPE_BF16, x_stride, pre_norm_w,
-                    KSL_DTYPE_BF16, pre_eps, H, a16, st);
+                    KSL_DTYPE_BF16, pre_eps, H, a16, bcnt, st);
     if (rc) return rc;
     rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
     if (rc) return rc;
@@ -421,15 +428,26 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
                                post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);
 }
 
+extern "C" size_t ksl_moe_route_scratch_bytes(int64_t T, int64_t topk, int64_t E) {
+    if (T < 0 || topk <= 0 || E <= 0) return 0;
+    const int64_t nexp = T * topk;
+    return nexp > 4096 ? static_cast<size_t>((nexp + 4095) / 4096 * E * 4) : 0;
+}
+
 extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
                                    int32_t* sorted_rows, int32_t* offsets, int32_t* inv, const void* x,
                                    int x_dtype, int64_t x_stride, const void* norm_w, int norm_w_dtype,
-                                   float eps, int64_t H, void* a16, void* stream) {
+                                   float eps, int64_t H, void* a16, void* scratch, size_t scratch_bytes,
+                                   void* stream) {
+    const size_t need = ksl_moe_route_scratch_bytes(T, topk, E);
+    int32_t* bcnt = need > 0 && scratch && scratch_bytes >= need && reinterpret_cast<uintptr_t>(scratch) % 4 == 0
+                        ? static_cast<int32_t*>(scratch)
+                        : nullptr;
     return ksl::route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
-                           norm_w_dtype, eps, H, a16, static_cast<hipStream_t>(stream));
+                           norm_w_dtype, eps, H, a16, bcnt, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int ksl_version(void) { return 2; }
+extern "C" int ksl_version(void) { return 3; }
 
 extern "C" const char* ksl_status_string(int status) {
     switch (status) {

@@ -186,6 +186,45 @@ __device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, i
         for (int p = before + lane; p < Nexp; p += kWave) sorted_rows[p] = Nexp;
 }
 
+// Activation prep by workgroup blk of nblk: hidden -> fp16, 8-blocks in K-slot order.
+template <int HD>
+__device__ __forceinline__ void prep_rows(int blk, int nblk, const void* __restrict__ hidden, int64_t hidden_stride,
+                                          int64_t T, int64_t H, f16* __restrict__ a16) {
+    typedef typename Elem<HD>::T HT;
+    const HT* h = static_cast<const HT*>(hidden);
+    const int64_t vec_per_row = H / 8;
+    const int64_t nvec = T * vec_per_row;
+    const int64_t nthreads = static_cast<int64_t>(nblk) * kRouteThreads;
+    for (int64_t v = static_cast<int64_t>(blk) * kRouteThreads + threadIdx.x; v < nvec; v += nthreads) {
+        const int64_t t = v / vec_per_row;
+        const int64_t c0 = (v - t * vec_per_row) * 8;
+        float f[8];
+        load8<HD>(h + t * hidden_stride + c0, f);
+        store_act8(a16 + t * H, static_cast<int>(c0), f);
+    }
+}
+
+// RMSNorm rows by workgroup blk of nblk: one wave per row (64 lanes x 8
+// columns x NSTEP), the bf16-rounded norm output converted to fp16 in the
+// gate/up activation order.
+template <int XD, int WD, int NSTEP, bool HAS_W>
+__device__ __forceinline__ void norm_rows(int blk, int nblk, const void* __restrict__ xv, int64_t x_stride,
+                                          const void* __restrict__ wv, float eps, int64_t T, int64_t H,
+                                          f16* __restrict__ a16) {
+    typedef typename Elem<XD>::T XT;
+    typedef typename Elem<WD>::T WT;
+    const XT* x = static_cast<const XT*>(xv);
+    const WT* w = static_cast<const WT*>(wv);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t nworkers = static_cast<int64_t>(nblk) * kRouteWaves;
+    for (int64_t row = static_cast<int64_t>(blk) * kRouteWaves + wave; row < T; row += nworkers) {
+        f16* arow = a16 + row * H;
+        rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true,
+                                      [&](int, int c0, const float (&v)[8]) { store_act8(arow, c0, v); });
+    }
+}
+
 template <typename IdxT, int HD>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const int64_t* __restrict__ ids, RouteOut R, IdxT* __restrict__ sorted_rows,
@@ -194,20 +233,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const void* __restrict__ hidden, int64_t hidden_stride, int64_t T, int64_t H,
     f16* __restrict__ a16) {
     if (blockIdx.x > 0) {
-        // ---- activation prep: hidden -> fp16, 8-blocks in K-slot order ----
-        typedef typename Elem<HD>::T HT;
-        const HT* h = static_cast<const HT*>(hidden);
-        const int64_t vec_per_row = H / 8;
-        const int64_t nvec = T * vec_per_row;
-        const int64_t nthreads = static_cast<int64_t>(gridDim.x - 1) * kRouteThreads;
-        for (int64_t v = static_cast<int64_t>(blockIdx.x - 1) * kRouteThreads + threadIdx.x; v < nvec;
-             v += nthreads) {
-            const int64_t t = v / vec_per_row;
-            const int64_t c0 = (v - t * vec_per_row) * 8;
-            float f[8];
-            load8<HD>(h + t * hidden_stride + c0, f);
-            store_act8(a16 + t * H, static_cast<int>(c0), f);
-        }
+        prep_rows<HD>(blockIdx.x - 1, gridDim.x - 1, hidden, hidden_stride, T, H, a16);
         return;
     }
     route_block<IdxT>(ids, R, sorted_rows, expert_ids, inv, offsets);
@@ -226,18 +252,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_norm_kernel(
         route_block<int32_t>(ids, R, sorted_rows, nullptr, inv, offsets);
         return;
     }
-    typedef typename Elem<XD>::T XT;
-    typedef typename Elem<WD>::T WT;
-    const XT* x = static_cast<const XT*>(xv);
-    const WT* w = static_cast<const WT*>(wv);
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int64_t nworkers = static_cast<int64_t>(gridDim.x - 1) * kRouteWaves;
-    for (int64_t row = static_cast<int64_t>(blockIdx.x - 1) * kRouteWaves + wave; row < T; row += nworkers) {
-        f16* arow = a16 + row * H;
-        rms_row<XD, WD, NSTEP, HAS_W>(x + row * x_stride, w, static_cast<int>(H), eps, lane, 6, true,
-                                      [&](int, int c0, const float (&v)[8]) { store_act8(arow, c0, v); });
-    }
+    norm_rows<XD, WD, NSTEP, HAS_W>(blockIdx.x - 1, gridDim.x - 1, xv, x_stride, wv, eps, T, H, a16);
 }
 
 // Fast compact routing (at most kFastRows rows) and the activation prep in one
@@ -409,6 +424,151 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
     }
 }
 
+// ---- multi-block compact routing (more than kFastRows rows, a workspace for
+// the block counts): the single-workgroup algorithm above with its waves
+// spread over blocks of kMbRows rows. Launch 1: every block counts its rows
+// per expert (wave w of block b owns rows b*kMbRows + w*256 .. +256, four
+// 64-row segments held in registers) and writes the block's counts to
+// bcnt[b*E + e]. Launch 2: every block counts again, adds the counts of the
+// blocks before it and of the lower experts (a scan over e of the column sums
+// of bcnt) to get each wave's first slot per expert, and places its rows in
+// row order, the stable order of the reference; block 0 writes offsets and
+// the unused tail slots.
+constexpr int kMbRows = kRouteWaves * kRouteSeg * kWave;
+
+__device__ __forceinline__ void mb_keys(const int64_t* __restrict__ ids, int64_t Nexp, int E, int64_t r_begin,
+                                        int (&keys)[kRouteSeg]) {
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int s = 0; s < kRouteSeg; ++s) {
+        const int64_t r = r_begin + s * kWave + lane;
+        const bool ok = r < Nexp;
+        const int64_t id = ids[ok ? r : 0];
+        keys[s] = !ok ? E + 1 : ((id < 0 || id > E) ? E : static_cast<int>(id));  // E + 1: not a row
+    }
+}
+
+// Per-wave counts of the block's rows into wcnt[wave][e] (zeroed here).
+__device__ __forceinline__ void mb_wave_counts(const int (&keys)[kRouteSeg], int E, int nbits, int32_t* wcnt) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    for (int i = threadIdx.x; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
+    __syncthreads();
+    int32_t* mycnt = wcnt + wave * E;
+#pragma unroll
+    for (int s = 0; s < kRouteSeg; ++s) {
+        const uint64_t peers = match_key(keys[s], nbits);
+        if (__builtin_ctzll(peers) == lane && keys[s] < E) mycnt[keys[s]] += __builtin_popcountll(peers);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int mb_nbits(int E) {
+    int nbits = 1;
+    while ((1 << nbits) < E + 2) ++nbits;  // keys 0..E+1
+    return nbits;
+}
+
+__device__ void route_mb_count(const int64_t* __restrict__ ids, int64_t Nexp, int E, int b,
+                               int32_t* __restrict__ bcnt) {
+    extern __shared__ int32_t lds[];
+    const int wave = threadIdx.x / kWave;
+    int keys[kRouteSeg];
+    mb_keys(ids, Nexp, E, static_cast<int64_t>(b) * kMbRows + wave * (kRouteSeg * kWave), keys);
+    mb_wave_counts(keys, E, mb_nbits(E), lds);
+    for (int e = threadIdx.x; e < E; e += kRouteThreads) {
+        int32_t c = 0;
+        for (int w = 0; w < kRouteWaves; ++w) c += lds[w * E + e];
+        bcnt[static_cast<int64_t>(b) * E + e] = c;
+    }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
+    const int64_t* __restrict__ ids, int64_t Nexp, int E, int nb, const int32_t* __restrict__ bcnt,
+    int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv, int32_t* __restrict__ offsets) {
+    extern __shared__ int32_t lds[];
+    int32_t* wcnt = lds;                                                  // [kRouteWaves][E]
+    int64_t* estart = reinterpret_cast<int64_t*>(lds + kRouteWaves * E);  // [E]
+    int64_t* scan_tmp = estart + E;                                       // [kRouteWaves]
+    int64_t* total = scan_tmp + kRouteWaves;                              // [1]
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int b = blockIdx.x;
+    const int nbits = mb_nbits(E);
+    const int64_t r_begin = static_cast<int64_t>(b) * kMbRows + wave * (kRouteSeg * kWave);
+    int keys[kRouteSeg];
+    mb_keys(ids, Nexp, E, r_begin, keys);
+    mb_wave_counts(keys, E, nbits, wcnt);
+    // expert e (thread e): rows of all blocks, and of the blocks before b
+    const int e = threadIdx.x;
+    int64_t tot = 0;
+    if (e < E) {
+        int32_t pre = 0, all = 0;
+        for (int bb = 0; bb < nb; ++bb) {
+            const int32_t c = bcnt[static_cast<int64_t>(bb) * E + e];
+            all += c;
+            pre += bb < b ? c : 0;
+        }
+        tot = all;
+        int32_t run = pre;
+        for (int w = 0; w < kRouteWaves; ++w) {
+            const int32_t c = wcnt[w * E + e];
+            wcnt[w * E + e] = run;
+            run += c;
+        }
+    }
+    const int64_t start = block_exclusive_scan(e < E ? tot : 0, scan_tmp, total);
+    if (e < E) estart[e] = start;
+    if (b == 0) {
+        if (e < E) offsets[e] = static_cast<int32_t>(start);
+        if (threadIdx.x == 0) offsets[E] = static_cast<int32_t>(*total);
+        for (int64_t p = *total + threadIdx.x; p < Nexp; p += kRouteThreads) sorted_rows[p] = static_cast<int32_t>(Nexp);
+    }
+    __syncthreads();
+    int32_t* mycnt = wcnt + wave * E;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int s = 0; s < kRouteSeg; ++s) {
+        const int64_t r = r_begin + s * kWave + lane;
+        const int key = keys[s];
+        const uint64_t peers = match_key(key, nbits);
+        if (key < E) {
+            const int32_t before = mycnt[key];
+            const int64_t slot = estart[key] + before + __builtin_popcountll(peers & lt_mask);
+            sorted_rows[slot] = static_cast<int32_t>(r);
+            inv[r] = static_cast<int32_t>(slot);
+            if (__builtin_ctzll(peers) == lane) mycnt[key] = before + __builtin_popcountll(peers);
+        } else if (key == E) {
+            inv[r] = 0;
+        }
+    }
+}
+
+// Launch 1 of the multi-block routing with the RMSNorm rows (workgroups >= nb).
+template <int XD, int WD, int NSTEP, bool HAS_W>
+__global__ __launch_bounds__(kRouteThreads) void route_norm_mb_kernel(
+    const int64_t* __restrict__ ids, int64_t Nexp, int E, int nb, int32_t* __restrict__ bcnt,
+    const void* __restrict__ xv, int64_t x_stride, const void* __restrict__ wv, float eps, int64_t T, int64_t H,
+    f16* __restrict__ a16) {
+    if (static_cast<int>(blockIdx.x) < nb) {
+        route_mb_count(ids, Nexp, E, blockIdx.x, bcnt);
+        return;
+    }
+    norm_rows<XD, WD, NSTEP, HAS_W>(blockIdx.x - nb, gridDim.x - nb, xv, x_stride, wv, eps, T, H, a16);
+}
+
+// Launch 1 of the multi-block routing with the activation prep (workgroups >= nb).
+template <int HD>
+__global__ __launch_bounds__(kRouteThreads) void route_mb_kernel(
+    const int64_t* __restrict__ ids, int64_t Nexp, int E, int nb, int32_t* __restrict__ bcnt,
+    const void* __restrict__ hidden, int64_t hidden_stride, int64_t T, int64_t H, f16* __restrict__ a16) {
+    if (static_cast<int>(blockIdx.x) < nb) {
+        route_mb_count(ids, Nexp, E, blockIdx.x, bcnt);
+        return;
+    }
+    if (a16) prep_rows<HD>(blockIdx.x - nb, gridDim.x - nb, hidden, hidden_stride, T, H, a16);
+}
+
 size_t route_lds_bytes(int64_t E) {
     return kRouteWaves * E * sizeof(int32_t) + (E + kRouteWaves + 1) * sizeof(int64_t);
 }
@@ -456,7 +616,7 @@ extern "C" int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, i
 namespace ksl {
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
-                  int64_t H, void* a16, hipStream_t st) {
+                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st) {
     if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
     if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     if (T > 0 && !ids) return KSL_ERR_ARG;
@@ -490,6 +650,39 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
         KSL_LAUNCH_CHECK();
         return KSL_OK;
     }
+    if (bcnt && Nexp > kFastRows) {
+        // multi-block routing: count (+ activation prep), then scatter
+        const int nb = static_cast<int>((Nexp + kMbRows - 1) / kMbRows);
+        int64_t nprep = 0;
+        if (a) {
+            nprep = (T * (H / 8) + kRouteThreads * 4 - 1) / (kRouteThreads * 4);
+            if (nprep > 2048) nprep = 2048;
+        }
+        const dim3 grid(static_cast<unsigned>(nb + nprep)), block(kRouteThreads);
+        const size_t lds = route_lds_bytes(E);
+        const int e = static_cast<int>(E);
+        switch (hd) {
+            case KSL_DTYPE_BF16:
+                hipLaunchKernelGGL(route_mb_kernel<KSL_DTYPE_BF16>, grid, block, lds, st, ids, Nexp, e, nb, bcnt, hidden,
+                                   hstride, T, H, a);
+                break;
+            case KSL_DTYPE_F16:
+                hipLaunchKernelGGL(route_mb_kernel<KSL_DTYPE_F16>, grid, block, lds, st, ids, Nexp, e, nb, bcnt, hidden,
+                                   hstride, T, H, a);
+                break;
+            case KSL_DTYPE_F32:
+                hipLaunchKernelGGL(route_mb_kernel<KSL_DTYPE_F32>, grid, block, lds, st, ids, Nexp, e, nb, bcnt, hidden,
+                                   hstride, T, H, a);
+                break;
+            default:
+                return KSL_ERR_ARG;
+        }
+        KSL_LAUNCH_CHECK();
+        hipLaunchKernelGGL(route_mb_scatter_kernel, dim3(nb), block, lds, st, ids, Nexp, e, nb, bcnt, sorted_rows, inv,
+                           offsets);
+        KSL_LAUNCH_CHECK();
+        return KSL_OK;
+    }
     // compact layout: block_m = 1; slots past offsets[E] hold Nexp, only the
     // first Nexp slots are materialised.
     switch (hd) {
@@ -512,7 +705,7 @@ namespace {
 template <int XD, int WD, bool HAS_W>
 int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32_t* sorted_rows, int32_t* inv,
                          int32_t* offsets, const void* x, int64_t xs, const void* w, float eps, int64_t T,
-                         int64_t H, f16* a16, hipStream_t st) {
+                         int64_t H, f16* a16, int32_t* bcnt, hipStream_t st) {
     if (R.Nexp > 0 && R.Nexp <= kFastRows) {
         const int nrw = (R.E + 1 + kFastWaves - 1) / kFastWaves;
         const dim3 fgrid(static_cast<unsigned>(nrw + (T + kFastWaves - 1) / kFastWaves)), fblock(kFastWaves * kWave);
@@ -532,8 +725,27 @@ int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32
     int64_t want = (T + kRouteWaves - 1) / kRouteWaves;
     if (want < 1) want = 1;
     if (want > 4096) want = 4096;
-    const unsigned grid = 1 + static_cast<unsigned>(want);
     const size_t lds = route_lds_bytes(R.E);
+    if (bcnt && R.Nexp > kFastRows) {
+        // multi-block routing: count + norm rows, then scatter
+        const int nb = static_cast<int>((R.Nexp + kMbRows - 1) / kMbRows);
+        const dim3 mgrid(static_cast<unsigned>(nb + want));
+#define KSL_RNM(NS)                                                                                          \
+    hipLaunchKernelGGL((route_norm_mb_kernel<XD, WD, NS, HAS_W>), mgrid, dim3(kRouteThreads), lds, st, ids, R.Nexp, \
+                       R.E, nb, bcnt, x, xs, w, eps, T, H, a16)
+        if (nstep <= 1) KSL_RNM(1);
+        else if (nstep <= 2) KSL_RNM(2);
+        else if (nstep <= 4) KSL_RNM(4);
+        else if (nstep <= 6) KSL_RNM(6);
+        else KSL_RNM(8);
+#undef KSL_RNM
+        KSL_LAUNCH_CHECK();
+        hipLaunchKernelGGL(route_mb_scatter_kernel, dim3(nb), dim3(kRouteThreads), lds, st, ids, R.Nexp, R.E, nb, bcnt,
+                           sorted_rows, inv, offsets);
+        KSL_LAUNCH_CHECK();
+        return KSL_OK;
+    }
+    const unsigned grid = 1 + static_cast<unsigned>(want);
 #define KSL_RN(NS)                                                                                         \
     hipLaunchKernelGGL((route_norm_kernel<XD, WD, NS, HAS_W>), dim3(grid), dim3(kRouteThreads), lds, st, ids, R, \
                        sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16)
@@ -549,12 +761,12 @@ int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32
 template <int XD>
 int launch_route_norm_x(int wd, int nstep, const int64_t* ids, const RouteOut& R, int32_t* sorted_rows, int32_t* inv,
                         int32_t* offsets, const void* x, int64_t xs, const void* w, float eps, int64_t T,
-                        int64_t H, f16* a16, hipStream_t st) {
-    if (!w) return launch_route_norm_ns<XD, KSL_DTYPE_BF16, false>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+                        int64_t H, f16* a16, int32_t* bcnt, hipStream_t st) {
+    if (!w) return launch_route_norm_ns<XD, KSL_DTYPE_BF16, false>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, bcnt, st);
     switch (wd) {
-        case KSL_DTYPE_BF16: return launch_route_norm_ns<XD, KSL_DTYPE_BF16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
-        case KSL_DTYPE_F16: return launch_route_norm_ns<XD, KSL_DTYPE_F16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
-        case KSL_DTYPE_F32: return launch_route_norm_ns<XD, KSL_DTYPE_F32, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, st);
+        case KSL_DTYPE_BF16: return launch_route_norm_ns<XD, KSL_DTYPE_BF16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, bcnt, st);
+        case KSL_DTYPE_F16: return launch_route_norm_ns<XD, KSL_DTYPE_F16, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, bcnt, st);
+        case KSL_DTYPE_F32: return launch_route_norm_ns<XD, KSL_DTYPE_F32, true>(nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, bcnt, st);
     }
     return KSL_ERR_ARG;
 }
@@ -563,7 +775,7 @@ int launch_route_norm_x(int wd, int nstep, const int64_t* ids, const RouteOut& R
 // Routing plus RMSNorm -> fp16 activations in one launch (the layer path).
 int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
-               int wd, float eps, int64_t H, void* a16, hipStream_t st) {
+               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st) {
     if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
     if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     if (H <= 0 || H % 128 != 0 || H > 4096 || xs < H || xs % 8 != 0) return KSL_ERR_SHAPE;
@@ -576,8 +788,8 @@ int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* 
     const int nstep = static_cast<int>((H / 8 + kWave - 1) / kWave);
     f16* a = static_cast<f16*>(a16);
     switch (xd) {
-        case KSL_DTYPE_BF16: return launch_route_norm_x<KSL_DTYPE_BF16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, st);
-        case KSL_DTYPE_F16: return launch_route_norm_x<KSL_DTYPE_F16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, st);
+        case KSL_DTYPE_BF16: return launch_route_norm_x<KSL_DTYPE_BF16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, bcnt, st);
+        case KSL_DTYPE_F16: return launch_route_norm_x<KSL_DTYPE_F16>(wd, nstep, ids, R, sorted_rows, inv, offsets, x, xs, w, eps, T, H, a, bcnt, st);
     }
     return KSL_ERR_ARG;
 }
@@ -588,5 +800,5 @@ extern "C" int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, i
                              const void* hidden, int hidden_dtype, int64_t hidden_stride, int64_t H,
                              void* a16, void* stream) {
     return ksl::route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
-                              hidden_stride, H, a16, static_cast<hipStream_t>(stream));
+                              hidden_stride, H, a16, nullptr, static_cast<hipStream_t>(stream));
 }

@@ -87,6 +87,9 @@ class LayerRunner:
         self.out3 = torch.empty(nexp, H, dtype=torch.float16, device=device)
         self.y = torch.empty(T, H, dtype=act_dtype, device=device)
         self.lib = _lib.load()
+        # block counts of the multi-block routing (above 4096 routed rows)
+        self.scratch = torch.empty(max(1, int(self.lib.ksl_moe_route_scratch_bytes(T, topk, E)) // 4),
+                                   dtype=torch.int32, device=device)
 
     @torch.no_grad()
     def run(self, x, norm_w, eps, exp, topk_ids, topk_w, events=None):
@@ -103,7 +106,7 @@ class LayerRunner:
         rc = L.ksl_moe_layer_route(p(topk_ids), T, tk, E, p(self.sorted_rows), p(self.offsets), p(self.inv),
                                    p(x), code, x.stride(0), p(norm_w),
                                    _lib.dtype_code(norm_w.dtype) if norm_w is not None else code, float(eps),
-                                   H, p(self.a16), st)
+                                   H, p(self.a16), p(self.scratch), self.scratch.numel() * 4, st)
         _lib.check(rc, "ksl_moe_layer_route")
         if ev:
             ev[1].record()

@@ -26,7 +26,7 @@ def test_header_declares_the_entry_points():
     names = _declared()
     for n in ("ksl_rmsnorm", "ksl_moe_align", "ksl_moe_w4a16_forward", "ksl_moe_layer_forward",
               "ksl_moe_gateup_act", "ksl_moe_down", "ksl_moe_combine", "ksl_moe_router", "ksl_moe_combine_post",
-              "ksl_moe_block_forward", "ksl_version",
+              "ksl_moe_block_forward", "ksl_moe_route_scratch_bytes", "ksl_version",
               "ksl_status_string"):
         assert n in names
 
@@ -57,6 +57,17 @@ def test_host_only_calls(L):
     # sorted rows, offsets, inv, a16, out2, out3 at least
     assert a >= 256 * 8 * (704 + 2816) * 2 + 256 * 2816 * 2
     assert b > a
+
+
+def test_route_scratch_bytes(L):
+    # block counts of the multi-block routing: ceil(T*topk / 4096) * E int32, none up to 4096 rows
+    assert L.ksl_moe_route_scratch_bytes(512, 8, 128) == 0
+    assert L.ksl_moe_route_scratch_bytes(513, 8, 128) == 2 * 128 * 4
+    assert L.ksl_moe_route_scratch_bytes(8192, 8, 128) == 16 * 128 * 4
+    assert L.ksl_moe_route_scratch_bytes(-1, 8, 128) == 0
+    # the fused forward's workspace holds them after out3
+    base = L.ksl_moe_workspace_bytes(512, 8, 128, 2816, 704)
+    assert L.ksl_moe_workspace_bytes(513, 8, 128, 2816, 704) >= base + 2 * 128 * 4
 
 
 def test_validation_returns_before_device_work(L):

@@ -135,22 +135,27 @@ def test_route_compact_bit_exact(gpu, T, tk, E, seed, dropped):
 
 
 LAYER_ROUTE_CASES = [
-    # (T, tk, E, H, seed, dropped): routing + RMSNorm -> fp16 in one launch (ksl_moe_layer_route)
-    (256, 8, 128, 2816, 31, False),
-    (37, 3, 8, 256, 32, True),
-    (1, 8, 128, 2816, 33, False),
-    (600, 8, 128, 512, 34, True),
+    # (T, tk, E, H, seed, dropped, zipf, scratch): routing + RMSNorm -> fp16 (ksl_moe_layer_route);
+    # with scratch above 4096 routed rows the multi-block routing
+    (256, 8, 128, 2816, 31, False, None, False),
+    (37, 3, 8, 256, 32, True, None, False),
+    (1, 8, 128, 2816, 33, False, None, False),
+    (600, 8, 128, 512, 34, True, None, False),
+    (1025, 4, 60, 256, 35, True, None, True),       # 4100 rows: two blocks, the second of 4 rows
+    (8192, 8, 128, 2816, 36, True, 1.1, True),     # prefill: 65536 rows, Zipf popularity
+    (3000, 8, 512, 128, 37, True, None, True),     # the largest E
+    (8192, 8, 128, 2816, 36, True, 1.1, False),    # the same without scratch: one workgroup
 ]
 
 
-@pytest.mark.parametrize("T,tk,E,H,seed,dropped", LAYER_ROUTE_CASES)
-def test_layer_route_bit_exact(gpu, T, tk, E, H, seed, dropped):
-    """The layer's first launch: compact routing bit-exact vs the oracle and the
+@pytest.mark.parametrize("T,tk,E,H,seed,dropped,zipf,scratch", LAYER_ROUTE_CASES)
+def test_layer_route_bit_exact(gpu, T, tk, E, H, seed, dropped, zipf, scratch):
+    """The layer's first stage: compact routing bit-exact vs the oracle and the
     fp16 activations equal to fp16(fused_rmsnorm(x)) in the gate/up order."""
     lib = load_pkg()._lib
     frm = load_mod("fused_rmsnorm")
     wl = load_mod("workloads")
-    ids, _ = wl.make_routing(T, E, tk, seed)
+    ids, _ = wl.make_routing(T, E, tk, seed, zipf)
     ids = ids.clone()
     if dropped:
         ids[0, 0] = E
@@ -162,10 +167,12 @@ def test_layer_route_bit_exact(gpu, T, tk, E, H, seed, dropped):
     off = torch.empty(E + 1, dtype=torch.int32, device=gpu)
     inv = torch.empty(T * tk, dtype=torch.int32, device=gpu)
     a16 = torch.empty(T, H, dtype=torch.float16, device=gpu)
-    print(f"layer_route T={T} topk={tk} E={E} H={H}", flush=True)
+    nscr = int(lib.load().ksl_moe_route_scratch_bytes(T, tk, E)) if scratch else 0
+    scr = torch.full((max(1, nscr // 4),), -7, dtype=torch.int32, device=gpu)
+    print(f"layer_route T={T} topk={tk} E={E} H={H} scratch {nscr} B", flush=True)
     rc = lib.load().ksl_moe_layer_route(lib.ptr(idsg), T, tk, E, lib.ptr(sr), lib.ptr(off), lib.ptr(inv),
                                         lib.ptr(xg), lib.DTYPE_BF16, H, lib.ptr(nwg), lib.DTYPE_BF16, 1e-6, H,
-                                        lib.ptr(a16), lib.stream_of(xg))
+                                        lib.ptr(a16), lib.ptr(scr) if scratch else None, nscr, lib.stream_of(xg))
     lib.check(rc, "ksl_moe_layer_route")
     xn = frm.fused_rmsnorm(xg, nwg, 1e-6)
     torch.cuda.synchronize()
@@ -176,6 +183,67 @@ def test_layer_route_bit_exact(gpu, T, tk, E, H, seed, dropped):
     assert np.array_equal(_np(inv), ref_inv)
     assert np.array_equal(_np(off), np.concatenate([[0], np.cumsum(counts)]))
     assert np.array_equal(act_unperm(f16_bits(a16.cpu()), 128), f16_bits(xn.cpu().to(torch.float16)))
+
+
+def test_fused_forward_multiblock_routing_in_workspace(gpu):
+    """ksl_moe_w4a16_forward above 4096 routed rows routes with the multi-block
+    kernels (block counts in its workspace) and converts the activations in the
+    same launch: the routing buffers at the head of the workspace
+    (sorted_rows i32[Nexp] | offsets i32[E+1] | inv i32[Nexp], 256-byte
+    aligned regions) equal the oracle's compact routing, and the output equals
+    the forward on a routing done by one workgroup (the same call below 4097
+    rows is not available, so the staged route with no scratch stands in)."""
+    lib = load_pkg()._lib
+    wl = load_mod("workloads")
+    L = lib.load()
+    T, tk, E, H, I = 1500, 8, 64, 256, 128
+    ids, w = wl.make_routing(T, E, tk, 38, 1.1)
+    ids = ids.clone()
+    ids[3, 1] = E
+    ids[T - 1, 0] = -1
+    hidden = wl.make_hidden(T, H, 39)
+    exp = wl.make_experts(E, H, I, 40, device=gpu)
+    hg, idsg, wg = hidden.to(gpu), ids.to(gpu), w.to(gpu)
+    nbytes = int(L.ksl_moe_workspace_bytes(T, tk, E, H, I))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    st = lib.stream_of(hg)
+    bufs = [lib.ptr(getattr(exp, k)) for k in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z")]
+    print(f"w4a16_forward multi-block routing T={T} topk={tk} E={E}", flush=True)
+    rc = L.ksl_moe_w4a16_forward(lib.ptr(hg), lib.DTYPE_BF16, H, lib.ptr(idsg), lib.ptr(wg), lib.DTYPE_F32, *bufs,
+                                 lib.DN_LAYOUT_REF, T, tk, E, H, I, lib.ACT_SILU, lib.ptr(y), lib.DTYPE_BF16, H,
+                                 lib.ptr(ws), nbytes, st)
+    lib.check(rc, "ksl_moe_w4a16_forward")
+    torch.cuda.synchronize()
+    nexp = T * tk
+    a256 = lambda n: (n + 255) // 256 * 256
+    wsc = ws.cpu()
+    sr = wsc[:nexp * 4].view(torch.int32).numpy()
+    o0 = a256(nexp * 4)
+    off = wsc[o0:o0 + (E + 1) * 4].view(torch.int32).numpy()
+    i0 = o0 + a256((E + 1) * 4)
+    inv = wsc[i0:i0 + nexp * 4].view(torch.int32).numpy()
+    ids_ref = ids.numpy().copy()
+    ids_ref[ids_ref < 0] = E  # dropped, as the kernels treat it (the oracle, like the reference, rejects it)
+    ref_sr, _, _, ref_inv = mo.moe_align(ids_ref, 1, E)
+    flat = ids_ref.reshape(-1)
+    counts = np.bincount(flat[flat < E], minlength=E)
+    assert np.array_equal(sr, ref_sr[:nexp])
+    assert np.array_equal(inv, ref_inv)
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(counts)]))
+    # the same forward staged on a one-workgroup routing
+    sr1, off1, inv1, a16 = _route(gpu, idsg, hg, E)
+    out2 = torch.empty(nexp, I, dtype=torch.float16, device=gpu)
+    out3 = torch.empty(nexp, H, dtype=torch.float16, device=gpu)
+    y1 = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    lib.check(L.ksl_moe_gateup_act(lib.ptr(a16), lib.ptr(sr1), lib.ptr(off1), T, tk, *bufs[:3], E, H, I,
+                                   lib.ACT_SILU, lib.ptr(out2), st), "ksl_moe_gateup_act")
+    lib.check(L.ksl_moe_down(lib.ptr(out2), lib.ptr(off1), *bufs[3:], E, H, I, nexp, lib.ptr(out3),
+                             lib.DN_LAYOUT_REF, st), "ksl_moe_down")
+    lib.check(L.ksl_moe_combine(lib.ptr(out3), lib.ptr(inv1), lib.ptr(wg), lib.DTYPE_F32, T, tk, H, lib.ptr(y1),
+                                lib.DTYPE_BF16, H, st), "ksl_moe_combine")
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
 
 
 # ----------------------------------------------------------- expert GEMMs
