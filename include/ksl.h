@@ -75,7 +75,7 @@ int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, i
 /* Workspace bytes the fused forward needs for these shapes: the routing
  * (sorted rows, offsets, inv), the fp16 activations, out2, out3 and the
  * per-block expert counts of the multi-block routing used above 4096 routed
- * rows. */
+ * rows. The workspace pointer must be 256-byte aligned (hipMalloc's is). */
 size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I);
 
 /* The whole W4A16 MoE forward, four launches (five above 4096 routed rows:
