@@ -505,7 +505,7 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // --------------------------------------------------------------------- down
 // Register-streamed kernel. A workgroup of kDnWaves waves owns one expert and
 // a range of its output columns (the expert's H columns split over
-// ceil(#CUs / E) workgroups); the expert's activation rows (out2, up to 32 per
+// ceil(#CUs / E) workgroups); the expert's activation rows (out2, up to 64 per
 // chunk) and the scale / zero rows of the workgroup's columns are copied into
 // LDS once (direct global->LDS loads), so each activation row is read once
 // per workgroup. Every wave then walks its 16-column tiles (tiles w, w+11, ...)
@@ -521,6 +521,7 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // takes an 8-byte load, the 64-group order. B = fp16((q - z) * s), the
 // reference's own dequantised weight (kernels/fused_moe_w4_v2.py:172-175).
 constexpr int kDnWaves = 11;
+constexpr int kDnMaxMt = 4;  // 16-row M tiles per row chunk of down (64 rows)
 constexpr int kDnThreads = kDnWaves * kWave;
 constexpr int kDnMaxG = 16;  // I <= 1024
 
@@ -548,10 +549,10 @@ struct DnArgs {
     int rb;                 // > 0: one workgroup per (block of rb rows of an expert, column split)
 };
 
-// LDS: activation blocks [kMaxMt][2G] (1 KB each, frag_pos order), then the
+// LDS: activation blocks [kDnMaxMt][2G] (1 KB each, frag_pos order), then the
 // s rows and the z rows ([nrows][G] fp16 each) of the workgroup's columns.
 inline size_t dn_lds_bytes(int G, int nrows) {
-    return static_cast<size_t>(kMaxMt) * 2 * G * kBlk + static_cast<size_t>(nrows) * G * 4;
+    return static_cast<size_t>(kDnMaxMt) * 2 * G * kBlk + static_cast<size_t>(nrows) * G * 4;
 }
 
 template <int G2, bool TAIL>
@@ -602,7 +603,7 @@ __device__ __forceinline__ void dn_wait_w(DnW<G2, TAIL>& w) {
 }
 
 template <int G2, bool TAIL, int MT>
-__device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[kMaxMt], const char* __restrict__ a_lds,
+__device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[MT], const char* __restrict__ a_lds,
                                         const f16* __restrict__ srow, const f16* __restrict__ zrow, int c, int fo,
                                         const NibConsts& kn) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
@@ -688,9 +689,9 @@ __device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a
                                            int colw, bool valid, int mrows, int col, int c, int fo,
                                            const NibConsts& kn) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-    f32x4 acc[kMaxMt];
+    f32x4 acc[MT];
 #pragma unroll
-    for (int t = 0; t < kMaxMt; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int rl = tile * 16 + col;  // row of dn within the workgroup's columns
     dn_tile<G2, TAIL, MT>(w, acc, a_lds, s_lds + rl * G, z_lds + rl * G, c, fo, kn);
 #pragma unroll
@@ -755,7 +756,7 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     const int fo = frag_pos(col, c) * 16;
     const NibConsts kn = nib_consts();
     char* a_lds = lds;
-    f16* s_lds = reinterpret_cast<f16*>(lds + kMaxMt * 2 * G * kBlk);
+    f16* s_lds = reinterpret_cast<f16*>(lds + kDnMaxMt * 2 * G * kBlk);
     f16* z_lds = s_lds + ncols * G;
     const int64_t row0 = static_cast<int64_t>(e) * A.H + col0;  // first dn row of the workgroup
     const int rb = A.I >> 1;
@@ -769,8 +770,8 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
             const int q = q0 + lane;
             if (q < 2 * nq) dma16(q < nq ? ssrc + q * 16 : zsrc + (q - nq) * 16, reinterpret_cast<char*>(s_lds) + q0 * 16);
         }
-        const int mrows = M < 16 * kMaxMt ? M : 16 * kMaxMt;
-        dn_stage_a<G2, TAIL>(A, a_lds, start, 0, mrows, mrows > 16 ? 2 : 1, wave, rr, ch);
+        const int mrows = M < 16 * kDnMaxMt ? M : 16 * kDnMaxMt;
+        dn_stage_a<G2, TAIL>(A, a_lds, start, 0, mrows, (mrows + 15) >> 4, wave, rr, ch);
     }
     // 2. the first tile's weights, then wait for the LDS copies only
     DnW<G2, TAIL> w0, w1;
@@ -778,23 +779,26 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     vm_wait<0>();
     dma_barrier();
     const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDnWaves + 1 : 0;
-    for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
-        const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+    for (int m0 = 0; m0 < M; m0 += 16 * kDnMaxMt) {
+        const int mrows = M - m0 < 16 * kDnMaxMt ? M - m0 : 16 * kDnMaxMt;
+        const int mt = (mrows + 15) >> 4;
         if (m0 > 0) {
             __syncthreads();  // every wave is done with the previous chunk's activations
-            dn_stage_a<G2, TAIL>(A, a_lds, start, m0, mrows, mrows > 16 ? 2 : 1, wave, rr, ch);
+            dn_stage_a<G2, TAIL>(A, a_lds, start, m0, mrows, mt, wave, rr, ch);
             if (wave < ntiles) dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, col, c, rb);
             vm_wait<0>();
             dma_barrier();
         }
         const __amdgpu_buffer_rsrc_t out =
             raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
-        if (mrows > 16)
-            dn_tiles<G2, TAIL, 2, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
-                                  fo, kn);
-        else
-            dn_tiles<G2, TAIL, 1, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c,
-                                  fo, kn);
+#define KSL_DN_TILES(MT_)                                                                                      \
+    dn_tiles<G2, TAIL, MT_, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c, \
+                                    fo, kn)
+        if (mt == 1) KSL_DN_TILES(1);
+        else if (mt == 2) KSL_DN_TILES(2);
+        else if (mt == 3) KSL_DN_TILES(3);
+        else KSL_DN_TILES(4);
+#undef KSL_DN_TILES
     }
     vm_wait<0>();  // the last (repeated) prefetch lands before the wave ends
 }
