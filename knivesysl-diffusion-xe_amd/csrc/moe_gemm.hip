@@ -204,12 +204,12 @@ struct GuArgs {
     int rb;     // > 0: one workgroup per (block of rb rows of an expert, column block)
 };
 
-template <int NC, int NP, int R>
+template <int NC, int NP, int R, int MX = kMaxMt>
 struct GuShape {
     static constexpr int kCols = 16 * NC;                      // columns of I per workgroup
     static constexpr int kThreads = (NC + NP) * kWave;
     static constexpr int kSlotW = 2 * NC * kBlk;               // weight bytes per slot
-    static constexpr int kSlot = kSlotW + 4 * kMaxMt * kBlk;   // + activation bytes per slot
+    static constexpr int kSlot = kSlotW + 4 * MX * kBlk;       // + activation bytes per slot (MX M tiles)
     static constexpr int kSzPer = (4 * kCols * kGuMaxG * 2 / 16 + NC * kWave - 1) / (NC * kWave);
     static size_t lds_bytes(int G) { return static_cast<size_t>(R) * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
 };
@@ -221,9 +221,9 @@ struct GuShape {
 // Weight blocks of the first groups 0 .. min(R-1, G)-1 of a producer wave (the
 // blocks b = p + NP*k < 2*NC of gateup_produce), issued before the routing is
 // read: they do not depend on it.
-template <int NC, int NP, int R>
+template <int NC, int NP, int R, int MX>
 __device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int e, int c0, char* __restrict__ lds) {
-    using S = GuShape<NC, NP, R>;
+    using S = GuShape<NC, NP, R, MX>;
     const int lane = threadIdx.x & (kWave - 1);
     const int p = wave_id() - NC;
     const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
@@ -237,10 +237,10 @@ __device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int 
     }
 }
 
-template <int NC, int NP, int R, int MT>
+template <int NC, int NP, int R, int MX, int MT>
 __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
                                                int m0, int mrows, bool w_issued) {
-    using S = GuShape<NC, NP, R>;
+    using S = GuShape<NC, NP, R, MX>;
     constexpr int NB = 2 * NC + 4 * MT;
     constexpr int KP = (NB + NP - 1) / NP;
     const int lane = threadIdx.x & (kWave - 1);
@@ -308,10 +308,10 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
 }
 
 // Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
-template <int ACT, int NC, int NP, int R, int MT>
+template <int ACT, int NC, int NP, int R, int MX, int MT>
 __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
                                                const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
-    using S = GuShape<NC, NP, R>;
+    using S = GuShape<NC, NP, R, MX>;
     const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
@@ -331,19 +331,28 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();  // group 0 and the scale table are ready
     int slot = 0;
+    // With up to four M tiles (MX > 2, the row blocks of large routings) the
+    // scale is folded into the B operand, b = fp16((q - z) * s), the
+    // reference's own dequantised weight, and the MFMAs accumulate into acc
+    // directly: two tiles' fp32 group partials would not fit the registers.
+    constexpr bool kFold = MX > 2;
     for (int g = 0; g < G; ++g) {
         const char* sp = lds + slot * S::kSlot;
-        f32x4 part[2][MT];
+        f32x4 part[2][kFold ? 1 : MT];
+        if constexpr (!kFold) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
         u32x4 wv[2];
         ZeroPair zc[2];
+        f16 sv[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             wv[j] = *reinterpret_cast<const u32x4*>(sp + (wave * 2 + j) * kBlk + fo);
             zc[j] = zero_pair((j ? z_u : z_g)[r * G + g]);
+            if constexpr (kFold) sv[j] = (j ? s_u : s_g)[r * G + g];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -353,18 +362,29 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
                 a[t] = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
+                if constexpr (kFold) {
+                    const f16x8 b = nib8_dequant(wv[j][i], zc[j], f16x2{sv[j], sv[j]}, kn);
 #pragma unroll
-                for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
+                    for (int t = 0; t < MT; ++t) acc[j][t] = mfma16x16x32(a[t], b, acc[j][t]);
+                } else {
+                    const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
+                }
             }
+            // more than two M tiles: one 32-K step's fragments at a time
+            // (hoisting all four steps' activations would exceed 128 VGPRs)
+            if constexpr (MT > 2) __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (!kFold) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
+            for (int j = 0; j < 2; ++j) {
+                const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
+                for (int t = 0; t < MT; ++t)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
+                    for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
+            }
         }
         slot = slot + 1 == R ? 0 : slot + 1;
         __syncthreads();
@@ -384,9 +404,9 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     }
 }
 
-template <int ACT, int NC, int NP, int R>
+template <int ACT, int NC, int NP, int R, int MX>
 __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A) {
-    using S = GuShape<NC, NP, R>;
+    using S = GuShape<NC, NP, R, MX>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -398,7 +418,7 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
         if (M <= 0) return;  // past the last row block (uniform)
     } else {
         e = unit;
-        if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R>(A, e, c0, lds);
+        if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R, MX>(A, e, c0, lds);
         start = A.offsets[e];
         M = A.offsets[e + 1] - start;
         if (M <= 0) {
@@ -412,13 +432,17 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     // Roles split once; both loops run the same chunks with the same barrier
     // count (1 + G per chunk), and the ring is free after a chunk's last barrier.
     if (wave_id() >= NC) {
-        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
-            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+        for (int m0 = 0; m0 < M; m0 += 16 * MX) {
+            const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
             const bool w_issued = m0 == 0 && A.early;
             if (mrows <= 16)
-                gateup_produce<NC, NP, R, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
+                gateup_produce<NC, NP, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
+            else if (MX == 2 || mrows <= 32)
+                gateup_produce<NC, NP, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+            else if (mrows <= 48)
+                gateup_produce<NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
             else
-                gateup_produce<NC, NP, R, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                gateup_produce<NC, NP, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
         }
     } else {
         // scale / zero table of the workgroup's rows: four [kCols x G] fp16
@@ -443,12 +467,16 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
                 if (i < 4 * nq) reinterpret_cast<u32x4*>(lds_sz)[i] = v[k];
             }
         }
-        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
-            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+        for (int m0 = 0; m0 < M; m0 += 16 * MX) {
+            const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
             if (mrows <= 16)
-                gateup_consume<ACT, NC, NP, R, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+                gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+            else if (MX == 2 || mrows <= 32)
+                gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
+            else if (mrows <= 48)
+                gateup_consume<ACT, NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
             else
-                gateup_consume<ACT, NC, NP, R, 2>(A, c0, lds, lds_sz, start, m0, mrows);
+                gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
         }
     }
 }
@@ -480,22 +508,23 @@ int device_cus() {
     return n;
 }
 
-template <int NC, int NP, int R>
+template <int NC, int NP, int R, int MX = kMaxMt>
 int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStream_t st) {
-    using S = GuShape<NC, NP, R>;
+    using S = GuShape<NC, NP, R, MX>;
     // row blocks: at most ceil(nrows / rb) + E of them (one partial block per expert)
     const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
     if (units * (A.I / S::kCols) >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const unsigned grid = static_cast<unsigned>(units * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
     if (lds > kLdsBytes) return KSL_ERR_SHAPE;
-    static const bool attr_set = set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>)) &&
-                                 set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>));
+    static const bool attr_set =
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R, MX>)) &&
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R, MX>));
     (void)attr_set;
     if (act == KSL_ACT_GELU_TANH)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R, MX>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else if (act == KSL_ACT_SILU)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R, MX>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else
         return KSL_ERR_ARG;
     KSL_LAUNCH_CHECK();
@@ -873,6 +902,11 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // widest column block that divides I: 176 (11 consumers), 128, or 64
     // (ring depth 4 where the LDS holds it: 176 columns up to H = 3712)
     if (I % 176 == 0) {
+        // row blocks (prefill): chunks of up to 64 rows, four M tiles per
+        // decoded weight fragment, ring depth 3 (the slots hold 16 KB of
+        // activations)
+        if (A.rb > 0 && GuShape<11, 5, 3, 4>::lds_bytes(H / 128) <= kLdsBytes)
+            return launch_gateup_nc<11, 5, 3, 4>(A, E, nrows_hint, act, st);
         if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, nrows_hint, act, st);
         return launch_gateup_nc<11, 5, 3>(A, E, nrows_hint, act, st);
     }

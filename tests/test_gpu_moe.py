@@ -275,6 +275,7 @@ STAGE_CASES = [
     (256, 8, 128, 2816, 704, 33),
     (48, 4, 8, 384, 704, 34),    # odd number of 128-groups, 176-column blocks
     (40, 4, 4, 640, 128, 35),    # odd number of 128-groups, 128-column blocks
+    (1100, 8, 12, 256, 704, 36),  # 8800 rows: row blocks, chunks of up to 64 rows (four M tiles)
 ]
 
 
