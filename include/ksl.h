@@ -155,7 +155,7 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
  * stored at i*32 + c*8 + s(j). T: the tokens of a16 (T*topk routed rows;
  * with at least E of them the first weight groups are fetched before the
  * routing is read; above 8192 of them each workgroup takes a block of at most
- * 128 rows of one expert). */
+ * 64 rows of one expert). */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
                        int64_t T, int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
@@ -164,7 +164,7 @@ int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_
  * out3 fp16 [T*topk, H] row per sorted slot, natural column order, 8-byte
  * aligned (written 4 columns per store). nrows:
  * the routed rows (T*topk), which size the grid (above 8192 routed rows each
- * workgroup takes a block of at most 128 rows of one expert, so that a heavy
+ * workgroup takes a block of at most 64 rows of one expert, so that a heavy
  * expert spreads over many workgroups). dn_layout as in ksl_moe_w4a16_forward. */
 int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
                  const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,

@@ -32,7 +32,7 @@
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
 // rows (one or two 16-row M tiles); above 8192 routed rows one workgroup per
-// block of at most 128 rows of an expert. Workgroups are remapped so that all
+// block of at most 64 rows of an expert. Workgroups are remapped so that all
 // column blocks of an expert run on the same XCD (shared L2 for its
 // activations).
 #include <algorithm>
@@ -45,7 +45,7 @@ namespace ksl {
 namespace {
 
 constexpr int kXcds = 8;
-constexpr int kRowBlock = 128;       // rows per workgroup block of a large routing
+constexpr int kRowBlock = 64;        // rows per workgroup block of a large routing
 constexpr int kRowBlockFrom = 8192;  // routed rows above which experts split into row blocks
 
 // Index of the calling wave in its workgroup, in a scalar register (branches
