@@ -128,7 +128,7 @@ int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_
                         int64_t x_stride, const void* norm_w, int norm_w_dtype, float eps, int64_t H,
                         void* a16, void* scratch, size_t scratch_bytes, void* stream);
 
-/* Scratch bytes of the multi-block routing: ceil(T*topk / 4096) * E int32
+/* Scratch bytes of the multi-block routing: ceil(T*topk / 1024) * E int32
  * block counts (0 when T*topk <= 4096). Not a reference entry point. */
 size_t ksl_moe_route_scratch_bytes(int64_t T, int64_t topk, int64_t E);
 

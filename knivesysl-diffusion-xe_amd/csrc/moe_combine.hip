@@ -10,7 +10,7 @@
 namespace ksl {
 
 // bcnt: workspace for the per-block counts of the multi-block routing
-// (ceil(T*topk / 4096) * E int32), or null for the single-workgroup routing.
+// (ceil(T*topk / 1024) * E int32), or null for the single-workgroup routing.
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
                   int64_t H, void* a16, int32_t* bcnt, hipStream_t st);
@@ -269,7 +269,7 @@ int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int
 // Workspace layout of the fused forward (each region 256-byte aligned):
 //   sorted_rows i32[Nexp] | offsets i32[E+1] | inv i32[Nexp] |
 //   a16 f16[T*H] | out2 f16[Nexp*I] | out3 f16[Nexp*H] |
-//   bcnt i32[ceil(Nexp/4096) * E] (per-block expert counts of the multi-block routing)
+//   bcnt i32[ceil(Nexp/1024) * E] (per-block expert counts of the multi-block routing)
 struct MoeWorkspace {
     size_t sorted_rows, offsets, inv, a16, out2, out3, bcnt, total;
 };
@@ -286,7 +286,7 @@ static MoeWorkspace moe_workspace_layout(int64_t T, int64_t topk, int64_t E, int
     w.a16 = off;         off += align256(static_cast<size_t>(T * H) * 2);
     w.out2 = off;        off += align256(nexp * static_cast<size_t>(I) * 2);
     w.out3 = off;        off += align256(nexp * static_cast<size_t>(H) * 2);
-    w.bcnt = off;        off += align256((nexp + 4095) / 4096 * static_cast<size_t>(E) * 4);
+    w.bcnt = off;        off += align256((nexp + 1023) / 1024 * static_cast<size_t>(E) * 4);
     w.total = off;
     return w;
 }
@@ -431,7 +431,7 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
 extern "C" size_t ksl_moe_route_scratch_bytes(int64_t T, int64_t topk, int64_t E) {
     if (T < 0 || topk <= 0 || E <= 0) return 0;
     const int64_t nexp = T * topk;
-    return nexp > 4096 ? static_cast<size_t>((nexp + 4095) / 4096 * E * 4) : 0;
+    return nexp > 4096 ? static_cast<size_t>((nexp + 1023) / 1024 * E * 4) : 0;
 }
 
 extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,

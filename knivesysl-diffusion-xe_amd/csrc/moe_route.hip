@@ -426,21 +426,22 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
 
 // ---- multi-block compact routing (more than kFastRows rows, a workspace for
 // the block counts): the single-workgroup algorithm above with its waves
-// spread over blocks of kMbRows rows. Launch 1: every block counts its rows
-// per expert (wave w of block b owns rows b*kMbRows + w*256 .. +256, four
-// 64-row segments held in registers) and writes the block's counts to
+// spread over blocks of kMbRows = 1024 rows. Launch 1: every block counts its
+// rows per expert (wave w of block b owns rows b*kMbRows + w*64 .. +64, one
+// 64-row segment held in registers) and writes the block's counts to
 // bcnt[b*E + e]. Launch 2: every block counts again, adds the counts of the
 // blocks before it and of the lower experts (a scan over e of the column sums
 // of bcnt) to get each wave's first slot per expert, and places its rows in
 // row order, the stable order of the reference; block 0 writes offsets and
 // the unused tail slots.
-constexpr int kMbRows = kRouteWaves * kRouteSeg * kWave;
+constexpr int kMbSeg = 1;  // 64-row segments per wave
+constexpr int kMbRows = kRouteWaves * kMbSeg * kWave;
 
 __device__ __forceinline__ void mb_keys(const int64_t* __restrict__ ids, int64_t Nexp, int E, int64_t r_begin,
-                                        int (&keys)[kRouteSeg]) {
+                                        int (&keys)[kMbSeg]) {
     const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-    for (int s = 0; s < kRouteSeg; ++s) {
+    for (int s = 0; s < kMbSeg; ++s) {
         const int64_t r = r_begin + s * kWave + lane;
         const bool ok = r < Nexp;
         const int64_t id = ids[ok ? r : 0];
@@ -449,14 +450,14 @@ __device__ __forceinline__ void mb_keys(const int64_t* __restrict__ ids, int64_t
 }
 
 // Per-wave counts of the block's rows into wcnt[wave][e] (zeroed here).
-__device__ __forceinline__ void mb_wave_counts(const int (&keys)[kRouteSeg], int E, int nbits, int32_t* wcnt) {
+__device__ __forceinline__ void mb_wave_counts(const int (&keys)[kMbSeg], int E, int nbits, int32_t* wcnt) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     for (int i = threadIdx.x; i < kRouteWaves * E; i += kRouteThreads) wcnt[i] = 0;
     __syncthreads();
     int32_t* mycnt = wcnt + wave * E;
 #pragma unroll
-    for (int s = 0; s < kRouteSeg; ++s) {
+    for (int s = 0; s < kMbSeg; ++s) {
         const uint64_t peers = match_key(keys[s], nbits);
         if (__builtin_ctzll(peers) == lane && keys[s] < E) mycnt[keys[s]] += __builtin_popcountll(peers);
     }
@@ -473,8 +474,8 @@ __device__ void route_mb_count(const int64_t* __restrict__ ids, int64_t Nexp, in
                                int32_t* __restrict__ bcnt) {
     extern __shared__ int32_t lds[];
     const int wave = threadIdx.x / kWave;
-    int keys[kRouteSeg];
-    mb_keys(ids, Nexp, E, static_cast<int64_t>(b) * kMbRows + wave * (kRouteSeg * kWave), keys);
+    int keys[kMbSeg];
+    mb_keys(ids, Nexp, E, static_cast<int64_t>(b) * kMbRows + wave * (kMbSeg * kWave), keys);
     mb_wave_counts(keys, E, mb_nbits(E), lds);
     for (int e = threadIdx.x; e < E; e += kRouteThreads) {
         int32_t c = 0;
@@ -495,8 +496,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
     const int wave = threadIdx.x / kWave;
     const int b = blockIdx.x;
     const int nbits = mb_nbits(E);
-    const int64_t r_begin = static_cast<int64_t>(b) * kMbRows + wave * (kRouteSeg * kWave);
-    int keys[kRouteSeg];
+    const int64_t r_begin = static_cast<int64_t>(b) * kMbRows + wave * (kMbSeg * kWave);
+    int keys[kMbSeg];
     mb_keys(ids, Nexp, E, r_begin, keys);
     mb_wave_counts(keys, E, nbits, wcnt);
     // expert e (thread e): rows of all blocks, and of the blocks before b
@@ -504,6 +505,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
     int64_t tot = 0;
     if (e < E) {
         int32_t pre = 0, all = 0;
+#pragma unroll 16
         for (int bb = 0; bb < nb; ++bb) {
             const int32_t c = bcnt[static_cast<int64_t>(bb) * E + e];
             all += c;
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
     int32_t* mycnt = wcnt + wave * E;
     const uint64_t lt_mask = (1ull << lane) - 1ull;
 #pragma unroll
-    for (int s = 0; s < kRouteSeg; ++s) {
+    for (int s = 0; s < kMbSeg; ++s) {
         const int64_t r = r_begin + s * kWave + lane;
         const int key = keys[s];
         const uint64_t peers = match_key(key, nbits);

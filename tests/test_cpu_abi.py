@@ -60,14 +60,14 @@ def test_host_only_calls(L):
 
 
 def test_route_scratch_bytes(L):
-    # block counts of the multi-block routing: ceil(T*topk / 4096) * E int32, none up to 4096 rows
+    # block counts of the multi-block routing: ceil(T*topk / 1024) * E int32, none up to 4096 rows
     assert L.ksl_moe_route_scratch_bytes(512, 8, 128) == 0
-    assert L.ksl_moe_route_scratch_bytes(513, 8, 128) == 2 * 128 * 4
-    assert L.ksl_moe_route_scratch_bytes(8192, 8, 128) == 16 * 128 * 4
+    assert L.ksl_moe_route_scratch_bytes(513, 8, 128) == 5 * 128 * 4
+    assert L.ksl_moe_route_scratch_bytes(8192, 8, 128) == 64 * 128 * 4
     assert L.ksl_moe_route_scratch_bytes(-1, 8, 128) == 0
     # the fused forward's workspace holds them after out3
     base = L.ksl_moe_workspace_bytes(512, 8, 128, 2816, 704)
-    assert L.ksl_moe_workspace_bytes(513, 8, 128, 2816, 704) >= base + 2 * 128 * 4
+    assert L.ksl_moe_workspace_bytes(513, 8, 128, 2816, 704) >= base + 5 * 128 * 4
 
 
 def test_validation_returns_before_device_work(L):

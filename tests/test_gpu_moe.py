@@ -141,7 +141,7 @@ LAYER_ROUTE_CASES = [
     (37, 3, 8, 256, 32, True, None, False),
     (1, 8, 128, 2816, 33, False, None, False),
     (600, 8, 128, 512, 34, True, None, False),
-    (1025, 4, 60, 256, 35, True, None, True),       # 4100 rows: two blocks, the second of 4 rows
+    (1025, 4, 60, 256, 35, True, None, True),       # 4100 rows: five blocks, the last of 4 rows
     (8192, 8, 128, 2816, 36, True, 1.1, True),     # prefill: 65536 rows, Zipf popularity
     (3000, 8, 512, 128, 37, True, None, True),     # the largest E
     (8192, 8, 128, 2816, 36, True, 1.1, False),    # the same without scratch: one workgroup
