@@ -36,7 +36,6 @@ constexpr int kRouteWaves = 16;
 constexpr int kRouteThreads = kRouteWaves * kWave;
 constexpr int kRouteSeg = 4;  // 64-row segments per wave per key batch
 constexpr int kMaxExperts = 512;  // 16 waves x E int32 counters + E int64 starts fit in 64 KB of LDS
-constexpr int kPrepThreads = 256;
 
 __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
     uint64_t peers = ~0ull;
