@@ -47,6 +47,7 @@ namespace {
 constexpr int kXcds = 8;
 constexpr int kRowBlock = 64;        // rows per workgroup block of a large routing
 constexpr int kRowBlockFrom = 8192;  // routed rows above which experts split into row blocks
+constexpr bool kGuRows128 = true;     // gate/up over row blocks: 12 waves, 128-row chunks and blocks
 
 // Index of the calling wave in its workgroup, in a scalar register (branches
 // on it are uniform).
@@ -307,6 +308,71 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
     }
 }
 
+// Producer side with a single producer wave (NP = 1, the 12-wave
+// configuration whose consumers hold eight M tiles): all 2*NC + 4*MT blocks of
+// a group from one wave, each address computed from a per-lane base (a wave
+// cannot keep one pointer per block in registers). Same slots, order and
+// barriers as gateup_produce.
+template <int NC, int R, int MX, int MT>
+__device__ __forceinline__ void gateup_produce_1w(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
+                                                  int m0, int mrows, bool w_issued) {
+    using S = GuShape<NC, 1, R, MX>;
+    constexpr int NB = 2 * NC + 4 * MT;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int G = A.H >> 7;
+    const int rowbytes = A.H >> 1;
+    // weights: the expert's first gate row of the column block, plus the lane's
+    // row and 16-byte piece; block (w, j) adds (j*I + w*16) rows
+    const char* wbase =
+        reinterpret_cast<const char*>(A.gu_q) + (static_cast<int64_t>(e) * 2 * A.I + c0) * rowbytes;
+    const int wlane = rr * rowbytes + ch * 16;
+    // activations: the lane's token row of each M tile (rows past the chunk
+    // repeat its last row: loaded, never stored)
+    const char* abase = reinterpret_cast<const char*>(A.a16);
+    int64_t aoff[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        int r = t * 16 + rr;
+        if (r >= mrows) r = mrows - 1;
+        const int tok = A.sorted_rows[start + m0 + r] / A.topk;
+        aoff[t] = (static_cast<int64_t>(tok) * A.H + ch * 8) * 2;
+    }
+    auto issue = [&](int g, int slot, bool wts) {
+        char* base = lds + slot * S::kSlot;
+        if (wts) {
+#pragma unroll
+            for (int b = 0; b < 2 * NC; ++b) {
+                const int w = b >> 1, j = b & 1;
+                dma16(wbase + static_cast<int64_t>((j ? A.I : 0) + w * 16) * rowbytes + wlane + g * 64,
+                      base + b * kBlk);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dma16(abase + aoff[t] + (i * 32 + g * 128) * 2, base + (2 * NC + t * 4 + i) * kBlk);
+    };
+    int issued = 0;
+    for (; issued < R - 1 && issued < G; ++issued) issue(issued, issued, !w_issued);
+    if (w_issued)
+        vm_wait<0>();
+    else
+        vm_wait_groups<NB, R - 2>(issued - 1);  // group 0 landed
+    dma_barrier();
+    int slot_next = issued % R;
+    for (int g = 0; g < G; ++g) {
+        if (issued < G) {
+            issue(issued, slot_next, true);
+            ++issued;
+            slot_next = slot_next + 1 == R ? 0 : slot_next + 1;
+        }
+        vm_wait_groups<NB, R - 2>(g + 1 < G ? issued - g - 2 : 0);
+        dma_barrier();
+    }
+}
+
 // Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
 template <int ACT, int NC, int NP, int R, int MX, int MT>
 __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
@@ -356,6 +422,21 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if constexpr (kFold && MT > 4) {
+                // eight M tiles: both decoded B fragments, then one activation
+                // fragment at a time (the accumulators take 64 registers)
+                f16x8 bb[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) bb[j] = nib8_dequant(wv[j][i], zc[j], f16x2{sv[j], sv[j]}, kn);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const f16x8 a1 = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
+                    acc[0][t] = mfma16x16x32(a1, bb[0], acc[0][t]);
+                    acc[1][t] = mfma16x16x32(a1, bb[1], acc[1][t]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                continue;
+            }
             f16x8 a[MT];
 #pragma unroll
             for (int t = 0; t < MT; ++t)
@@ -392,14 +473,16 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
     {
         const int sc = out2_store_index(c0 + wave * 16 + col, A.I & ~127);  // out2 is the down GEMM's activation
-        f16* o = A.out2 + static_cast<int64_t>(start + m0) * A.I + sc;
+        // the lane's part of the row offset (4c rows) in its pointer, the
+        // uniform part ((16t + q) rows) as a scalar offset
+        f16* o = A.out2 + (static_cast<int64_t>(start + m0) + 4 * c) * A.I + sc;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int row = t * 16 + 4 * c + q;
                 if (row < mrows)
-                    o[static_cast<int64_t>(row) * A.I] = static_cast<f16>(act_times_up<ACT>(acc[0][t][q], acc[1][t][q]));
+                    o[(t * 16 + q) * A.I] = static_cast<f16>(act_times_up<ACT>(acc[0][t][q], acc[1][t][q]));
             }
     }
 }
@@ -435,14 +518,25 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
         for (int m0 = 0; m0 < M; m0 += 16 * MX) {
             const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
             const bool w_issued = m0 == 0 && A.early;
-            if (mrows <= 16)
-                gateup_produce<NC, NP, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
-            else if (MX == 2 || mrows <= 32)
-                gateup_produce<NC, NP, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
-            else if (mrows <= 48)
-                gateup_produce<NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
-            else
-                gateup_produce<NC, NP, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
+            if constexpr (NP == 1) {
+                if (mrows <= 16)
+                    gateup_produce_1w<NC, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else if (mrows <= 32)
+                    gateup_produce_1w<NC, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else if (MX <= 4 || mrows <= 64)
+                    gateup_produce_1w<NC, R, MX, MX >= 4 ? 4 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else
+                    gateup_produce_1w<NC, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
+            } else {
+                if (mrows <= 16)
+                    gateup_produce<NC, NP, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else if (MX == 2 || mrows <= 32)
+                    gateup_produce<NC, NP, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else if (mrows <= 48)
+                    gateup_produce<NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                else
+                    gateup_produce<NC, NP, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
+            }
         }
     } else {
         // scale / zero table of the workgroup's rows: four [kCols x G] fp16
@@ -469,14 +563,25 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
         }
         for (int m0 = 0; m0 < M; m0 += 16 * MX) {
             const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
-            if (mrows <= 16)
-                gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
-            else if (MX == 2 || mrows <= 32)
-                gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
-            else if (mrows <= 48)
-                gateup_consume<ACT, NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
-            else
-                gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
+            if constexpr (NP == 1) {
+                if (mrows <= 16)
+                    gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+                else if (mrows <= 32)
+                    gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
+                else if (MX <= 4 || mrows <= 64)
+                    gateup_consume<ACT, NC, NP, R, MX, MX >= 4 ? 4 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
+                else
+                    gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
+            } else {
+                if (mrows <= 16)
+                    gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+                else if (MX == 2 || mrows <= 32)
+                    gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
+                else if (mrows <= 48)
+                    gateup_consume<ACT, NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
+                else
+                    gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
+            }
         }
     }
 }
@@ -762,6 +867,9 @@ __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, c
 template <int G2, bool TAIL, int LAYOUT>
 __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
+    // M tiles per chunk: four need more than the 168 registers of 11 waves
+    // once a tile's weights take G2 >= 6 128-K units (I >= 768)
+    constexpr int MTX = G2 >= 6 ? 2 : kDnMaxMt;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
     const int unit = bid / A.nsplit;  // expert, or row block when A.rb > 0
@@ -799,7 +907,7 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
             const int q = q0 + lane;
             if (q < 2 * nq) dma16(q < nq ? ssrc + q * 16 : zsrc + (q - nq) * 16, reinterpret_cast<char*>(s_lds) + q0 * 16);
         }
-        const int mrows = M < 16 * kDnMaxMt ? M : 16 * kDnMaxMt;
+        const int mrows = M < 16 * MTX ? M : 16 * MTX;
         dn_stage_a<G2, TAIL>(A, a_lds, start, 0, mrows, (mrows + 15) >> 4, wave, rr, ch);
     }
     // 2. the first tile's weights, then wait for the LDS copies only
@@ -808,8 +916,8 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     vm_wait<0>();
     dma_barrier();
     const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDnWaves + 1 : 0;
-    for (int m0 = 0; m0 < M; m0 += 16 * kDnMaxMt) {
-        const int mrows = M - m0 < 16 * kDnMaxMt ? M - m0 : 16 * kDnMaxMt;
+    for (int m0 = 0; m0 < M; m0 += 16 * MTX) {
+        const int mrows = M - m0 < 16 * MTX ? M - m0 : 16 * MTX;
         const int mt = (mrows + 15) >> 4;
         if (m0 > 0) {
             __syncthreads();  // every wave is done with the previous chunk's activations
@@ -823,10 +931,14 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
 #define KSL_DN_TILES(MT_)                                                                                      \
     dn_tiles<G2, TAIL, MT_, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c, \
                                     fo, kn)
-        if (mt == 1) KSL_DN_TILES(1);
-        else if (mt == 2) KSL_DN_TILES(2);
-        else if (mt == 3) KSL_DN_TILES(3);
-        else KSL_DN_TILES(4);
+        if (mt == 1) {
+            KSL_DN_TILES(1);
+        } else if (MTX == 2 || mt == 2) {
+            KSL_DN_TILES(2);
+        } else if constexpr (MTX == 4) {
+            if (mt == 3) KSL_DN_TILES(3);
+            else KSL_DN_TILES(4);
+        }
 #undef KSL_DN_TILES
     }
     vm_wait<0>();  // the last (repeated) prefetch lands before the wave ends
@@ -905,6 +1017,10 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
         // row blocks (prefill): chunks of up to 64 rows, four M tiles per
         // decoded weight fragment, ring depth 3 (the slots hold 16 KB of
         // activations)
+        if (A.rb > 0 && kGuRows128 && GuShape<11, 1, 2, 8>::lds_bytes(H / 128) <= kLdsBytes) {
+            A.rb = 128;
+            return launch_gateup_nc<11, 1, 2, 8>(A, E, nrows_hint, act, st);
+        }
         if (A.rb > 0 && GuShape<11, 5, 3, 4>::lds_bytes(H / 128) <= kLdsBytes)
             return launch_gateup_nc<11, 5, 3, 4>(A, E, nrows_hint, act, st);
         if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, nrows_hint, act, st);
