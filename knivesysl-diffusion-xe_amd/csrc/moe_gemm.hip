@@ -184,9 +184,11 @@ constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
 // block of 16 rows x 64 bytes. Blocks are fetched row-major (4 consecutive
 // lanes per 64-byte row: whole 64-byte segments per 4 lanes, which streams
 // faster than 16 rows per 4 lanes), and chunk c of row r sits at
-// r*4 + (c ^ (r/4 % 4)) so that the 16 lanes of one k-group read 16 distinct
-// 16-byte bank groups.
-__device__ __forceinline__ int frag_pos(int row, int c) { return row * 4 + (c ^ ((row >> 2) & 3)); }
+// r*4 + (c ^ swz(r)), swz(r) = (r/2 ^ 3*(r/8)) % 4, so that the 16 lanes of
+// one k-group cover all 64 four-byte banks and each 8 of them (rows 0-7,
+// 8-15) 32 distinct banks modulo 32.
+__device__ __forceinline__ int frag_swz(int row) { return ((row >> 1) ^ (row >> 3) * 3) & 3; }
+__device__ __forceinline__ int frag_pos(int row, int c) { return row * 4 + (c ^ frag_swz(row)); }
 constexpr size_t kLdsBytes = 160 * 1024;         // LDS per workgroup on gfx950
 constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
 constexpr int kGuMaxG = 32;                      // H <= 4096
@@ -227,7 +229,7 @@ __device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int 
     using S = GuShape<NC, NP, R, MX>;
     const int lane = threadIdx.x & (kWave - 1);
     const int p = wave_id() - NC;
-    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
     const int G = A.H >> 7;
     const int n0 = R - 1 < G ? R - 1 : G;
     for (int b = p; b < 2 * NC; b += NP) {
@@ -248,7 +250,7 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
     const int p = wave_id() - NC;
     // row-major fetch: lanes 4r .. 4r+3 cover the 64 bytes of block row r
     // (4 rows per 256 B), chunk order swizzled per row (frag_pos)
-    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
     const int G = A.H >> 7;
     const bool full = p + NP * (KP - 1) < NB;  // this wave issues KP blocks per group, else KP - 1
     const char* src[KP];
@@ -319,7 +321,7 @@ __device__ __forceinline__ void gateup_produce_1w(const GuArgs& A, int e, int c0
     using S = GuShape<NC, 1, R, MX>;
     constexpr int NB = 2 * NC + 4 * MT;
     const int lane = threadIdx.x & (kWave - 1);
-    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
     const int G = A.H >> 7;
     const int rowbytes = A.H >> 1;
     // weights: the expert's first gate row of the column block, plus the lane's
@@ -889,7 +891,7 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
-    const int rr = lane >> 2, ch = (lane & 3) ^ ((rr >> 2) & 3);
+    const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
     const int fo = frag_pos(col, c) * 16;
     const NibConsts kn = nib_consts();
     char* a_lds = lds;
