@@ -276,6 +276,10 @@ STAGE_CASES = [
     (48, 4, 8, 384, 704, 34),    # odd number of 128-groups, 176-column blocks
     (40, 4, 4, 640, 128, 35),    # odd number of 128-groups, 128-column blocks
     (1100, 8, 12, 256, 704, 36),  # 8800 rows: row blocks, chunks of up to 64 rows (four M tiles)
+    # I >= 768: down takes chunks of two M tiles (32 rows), experts of ~130-200 rows
+    (200, 2, 4, 256, 832, 38),    # 6.5 128-groups: a 64-K tail, 64-column gate/up blocks
+    (192, 2, 3, 256, 1024, 39),   # the largest I (16 64-groups)
+    (1100, 8, 12, 256, 768, 40),  # 8800 rows: row blocks with I >= 768
 ]
 
 
