@@ -644,7 +644,7 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // ceil(#CUs / E) workgroups); the expert's activation rows (out2, up to 64 per
 // chunk) and the scale / zero rows of the workgroup's columns are copied into
 // LDS once (direct global->LDS loads), so each activation row is read once
-// per workgroup. Every wave then walks its 16-column tiles (tiles w, w+11, ...)
+// per workgroup. Every wave then walks its 16-column tiles (tiles w, w+12, ...)
 // with the weights in registers, double buffered: the next tile's 16 rows x
 // I/2 bytes are loaded while the current tile is decoded and multiplied, and
 // all waves do MFMA and nibble decoding (down's decode, with the scale folded
@@ -656,7 +656,7 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // group of lane group c is 2*g2 + c/2. A trailing 64-K group (I % 128 == 64)
 // takes an 8-byte load, the 64-group order. B = fp16((q - z) * s), the
 // reference's own dequantised weight (kernels/fused_moe_w4_v2.py:172-175).
-constexpr int kDnWaves = 11;
+constexpr int kDnWaves = 12;
 constexpr int kDnMaxMt = 4;  // 16-row M tiles per row chunk of down (64 rows)
 constexpr int kDnThreads = kDnWaves * kWave;
 constexpr int kDnMaxG = 16;  // I <= 1024
@@ -859,6 +859,13 @@ __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, c
         dn_wait_w<kAfter>(w0);
         dn_do_tile<G2, TAIL, MT>(w0, a_lds, s_lds, z_lds, out, H, wave + k * kDnWaves, colw, true, mrows, col, c,
                                  fo, kn);
+        // odd count: tile k was the wave's last. w1's repeated load is waited
+        // for here, so its registers stay w1's until it has landed
+        // (wave-uniform branch)
+        if (k + 1 >= nmine) {
+            dn_wait_w<0>(w1);
+            break;
+        }
         dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave + k2 * kDnWaves) * 16 * rb, col, c, rb);
         dn_wait_w<kAfter>(w1);
         dn_do_tile<G2, TAIL, MT>(w1, a_lds, s_lds, z_lds, out, H, wave + k1 * kDnWaves, colw, k + 1 < nmine, mrows,
@@ -869,7 +876,7 @@ __device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, c
 template <int G2, bool TAIL, int LAYOUT>
 __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-    // M tiles per chunk: four need more than the 168 registers of 11 waves
+    // M tiles per chunk: four need more than the 168 registers of 12 waves
     // once a tile's weights take G2 >= 6 128-K units (I >= 768)
     constexpr int MTX = G2 >= 6 ? 2 : kDnMaxMt;
     extern __shared__ __attribute__((aligned(16))) char lds[];
