@@ -1020,8 +1020,9 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // (thousands of rows at prefill) spreads over many workgroups
     A.rb = nrows_hint > kRowBlockFrom ? kRowBlock : 0;
     if (A.rb > 0) A.early = 0;
-    // widest column block that divides I: 176 (11 consumers), 128, or 64
-    // (ring depth 4 where the LDS holds it: 176 columns up to H = 3712)
+    // widest column block that divides I: 176 (11 consumers), 128, or 64.
+    // One workgroup per expert with 176 columns: 11 consumers and one
+    // producer wave (12 waves, 3 per SIMD), ring depth 3
     if (I % 176 == 0) {
         // row blocks (prefill): chunks of up to 64 rows, four M tiles per
         // decoded weight fragment, ring depth 3 (the slots hold 16 KB of
@@ -1032,7 +1033,8 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
         }
         if (A.rb > 0 && GuShape<11, 5, 3, 4>::lds_bytes(H / 128) <= kLdsBytes)
             return launch_gateup_nc<11, 5, 3, 4>(A, E, nrows_hint, act, st);
-        if (GuShape<11, 5, 4>::lds_bytes(H / 128) <= kLdsBytes) return launch_gateup_nc<11, 5, 4>(A, E, nrows_hint, act, st);
+        if (GuShape<11, 1, 3>::lds_bytes(H / 128) <= kLdsBytes)
+            return launch_gateup_nc<11, 1, 3>(A, E, nrows_hint, act, st);
         return launch_gateup_nc<11, 5, 3>(A, E, nrows_hint, act, st);
     }
     if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, nrows_hint, act, st);
