@@ -73,6 +73,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--skip-kernel-pass", action="store_true")
+    ap.add_argument("--ffn", action="store_true",
+                    help="pack the weights so gate/up and down run as one launch")
     ap.add_argument("--skip-prefill", action="store_true",
                     help="skip the prefill_8192 (Zipf routing) layer timing and its MFMA utilisation")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -116,6 +118,8 @@ def main() -> int:
         v2._check_act(exp)
         v2._check_weights(exp, E, H, I)
         v2.enable_tiled_down(exp)  # load-time repack of the down weights (same results)
+        if args.ffn:
+            v2.enable_pack(exp)    # load-time pack for the one-launch expert FFN (same results)
     torch.cuda.synchronize()
 
     def step(exp):
@@ -123,7 +127,8 @@ def main() -> int:
         rc = L.ksl_moe_layer_forward(p(xg), lib.DTYPE_BF16, H, p(nwg), lib.DTYPE_BF16, 1e-6,
                                      p(idsg), p(wg), lib.DTYPE_F32,
                                      p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z),
-                                     lib.DN_LAYOUT_TILED, T, TOPK, E, H, I, exp._ksl_act, p(y), lib.DTYPE_BF16, H,
+                                     lib.DN_LAYOUT_TILED, *v2.pack_ptrs(exp), T, TOPK, E, H, I, exp._ksl_act, p(y),
+                                     lib.DTYPE_BF16, H,
                                      p(ws), ws.numel(), st)
         if rc:
             lib.check(rc, "ksl_moe_layer_forward")
@@ -152,7 +157,7 @@ def main() -> int:
     # ---- pass 2: per-kernel durations with events between launches ----------
     kernels = {}
     if not args.skip_kernel_pass:
-        stages = layer_mod.STAGES
+        stages = runner.stages(sets[0])
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(args.steps)]
         for i in range(args.warmup):
             runner.run(xg, nwg, 1e-6, sets[i % len(sets)], idsg, wg)
@@ -272,7 +277,8 @@ def main() -> int:
                 lib.check(rc, "ksl_moe_router")
             rc = L.ksl_moe_block_forward(p(xg), H, p(nwg), 1e-6, p(b_ids), p(b_w), lib.DTYPE_F32,
                                          p(exp0.gu_q), p(exp0.gu_s), p(exp0.gu_z), p(exp0.dn_q), p(exp0.dn_s),
-                                         p(exp0.dn_z), lib.DN_LAYOUT_TILED, T, TOPK, E, H, I, exp0._ksl_act, p(t_h1), H,
+                                         p(exp0.dn_z), lib.DN_LAYOUT_TILED, *v2.pack_ptrs(exp0), T, TOPK, E, H, I,
+                                         exp0._ksl_act, p(t_h1), H,
                                          p(t_w2), 1e-6,
                                          p(t_wp), 1e-6, p(t_ls), lib.DTYPE_BF16, p(b_y), H, p(ws), ws.numel(),
                                          stream)
@@ -366,7 +372,7 @@ def main() -> int:
         def pstep(exp):
             rc = L.ksl_moe_layer_forward(p(xpg), lib.DTYPE_BF16, H, p(nwpg), lib.DTYPE_BF16, 1e-6, p(idspg), p(wpg),
                                          lib.DTYPE_F32, p(exp.gu_q), p(exp.gu_s), p(exp.gu_z), p(exp.dn_q),
-                                         p(exp.dn_s), p(exp.dn_z), lib.DN_LAYOUT_TILED, Tp, TOPK, E, H, I,
+                                         p(exp.dn_s), p(exp.dn_z), lib.DN_LAYOUT_TILED, *v2.pack_ptrs(exp), Tp, TOPK, E, H, I,
                                          exp._ksl_act, p(yp), lib.DTYPE_BF16, H, p(wsp), wsp.numel(), st)
             if rc:
                 lib.check(rc, "ksl_moe_layer_forward")
@@ -383,12 +389,13 @@ def main() -> int:
         torch.cuda.synchronize()
         p_us = a.elapsed_time(b) * 1e3 / nrep
         prunner = layer_mod.LayerRunner(Tp, TOPK, E, H, I, dev)
-        pev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(layer_mod.STAGES) + 1)] for _ in range(nrep)]
+        pstages = prunner.stages(sets[0])
+        pev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(pstages) + 1)] for _ in range(nrep)]
         for i in range(nrep):
             prunner.run(xpg, nwpg, 1e-6, sets[i % len(sets)], idspg, wpg, events=pev[i])
         torch.cuda.synchronize()
         pk = {name: sum(pev[i][k].elapsed_time(pev[i][k + 1]) for i in range(nrep)) * 1e3 / nrep
-              for k, name in enumerate(layer_mod.STAGES)}
+              for k, name in enumerate(pstages)}
         tflops = flops / (p_us * 1e-6) / 1e12
         gemm_us = pk["gateup"] + pk["down"]
         prefill = {"tokens": Tp, "zipf_s": 1.1, "max_rows_per_expert": int(counts.max()),
@@ -405,7 +412,7 @@ def main() -> int:
     gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
-        gu_us = kernels["gateup"]["avg_us"]
+        gu_us = kernels["gateup"]["avg_us"] if "gateup" in kernels else kernels["ffn"]["avg_us"]
         ach = gu_bytes / (gu_us * 1e-6) / 1e9
         traffic = None
         tpath = os.path.join(ROOT, "profiles", "traffic_moe_gateup_layer256.json")

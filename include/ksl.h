@@ -91,11 +91,17 @@ size_t ksl_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, in
  * y: [T, H] of y_dtype with row stride y_stride. H % 128 == 0, I % 64 == 0
  * (fused_moe_w4_v2.py:327-328). dn_layout: KSL_DN_LAYOUT_REF, or
  * KSL_DN_LAYOUT_TILED for dn_q regrouped by ksl_moe_repack_down (same
- * results, faster weight stream). */
+ * results, faster weight stream).
+ * gu_pack / dn_pack: the same experts in the pack layout of ksl_moe_pack_gateup
+ * and ksl_moe_pack_down (16-byte aligned), or NULL. With both given and at
+ * most 8192 routed rows, gate/up and down run as ONE persistent launch over
+ * the pack layout (bit-identical results; gu_q .. dn_z are then not read and
+ * may be NULL); otherwise the gate/up and down launches read gu_q .. dn_z. */
 int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_stride,
                           const int64_t* topk_ids, const void* topk_w, int w_dtype,
                           const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                           const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                          const uint8_t* gu_pack, const uint8_t* dn_pack,
                           int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
                           void* y, int y_dtype, int64_t y_stride,
                           void* workspace, size_t workspace_bytes, void* stream);
@@ -108,12 +114,14 @@ int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64_t hidden_s
  * then gate/up, down and combine as in ksl_moe_w4a16_forward. x: bf16 or fp16
  * [T, H], row stride x_stride; H <= 4096. The normalised activations are
  * consumed in fp16 (bf16 norm output -> fp16, as hidden.to(fp16) does in
- * kernels/fused_moe_w4_v2.py:347). Same workspace as ksl_moe_w4a16_forward.
+ * kernels/fused_moe_w4_v2.py:347). Same workspace and weight arguments
+ * (gu_pack / dn_pack: three launches instead of four) as ksl_moe_w4a16_forward.
  * Not a reference entry point: the reference runs the two as separate calls. */
 int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
                           int norm_w_dtype, float eps, const int64_t* topk_ids, const void* topk_w,
                           int w_dtype, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout, int64_t T,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                          const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t T,
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                           int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -180,6 +188,55 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
  * H % 16 == 0, I % 64 == 0. */
 int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled, void* stream);
 
+/* Gate/up + activation and down of every expert in ONE persistent launch over
+ * the pack layout (the stage that ksl_moe_w4a16_forward runs between routing
+ * and combine when given gu_pack / dn_pack). Replaces _gateup_act_kernel and
+ * _down_kernel (kernels/fused_moe_w4_v2.py:96-177, launched at :351-366) with
+ * the same values: out2 and out3 are bit-identical to ksl_moe_gateup_act and
+ * ksl_moe_down. a16, sorted_rows, offsets as produced by ksl_moe_route /
+ * ksl_moe_layer_route; out2 fp16 [T*topk, I] (16-byte aligned), out3 fp16
+ * [T*topk, H] (8-byte aligned). ctl: ksl_moe_ffn_ctl_bytes(E) bytes of int32
+ * counters (one per 256 bytes: the unit queue, an error word, an exit count,
+ * one per expert) that must be zero on entry (torch.zeros once); the launch
+ * leaves them zero (the last workgroup to finish clears them), except the
+ * error word (int32 index 64), which becomes 1 if a wait for another
+ * workgroup ran out of its bound (then the output is not to be trusted). Calls that share one ctl
+ * buffer must not overlap. T*topk <= 8192, E <= 512, H % 128 == 0,
+ * I % 64 == 0, H, I <= 8192. */
+size_t ksl_moe_ffn_ctl_bytes(int64_t E);
+int ksl_moe_ffn(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t T, int64_t topk,
+                const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t E, int64_t H, int64_t I, int act,
+                void* out2, void* out3, int32_t* ctl, void* stream);
+
+/* Load-time pack of the experts for the one-launch expert FFN (the
+ * reference's precedent for a kernel-specific load-time repack is the
+ * preshuffled down pack, kernels/fused_moe_w4_v2.py:187-206). Out of place;
+ * the pack holds the same nibbles, scales and zero-points, regrouped so that
+ * each 128-K slot of a unit of work is one contiguous run of bytes:
+ *   gate/up, per expert e, unit cb (176 columns of I; the last unit of an
+ *   expert may be narrower: nt = min(11, I/16 - 11*cb) tiles), group g < H/128:
+ *   nt*2 blocks of 1 KB (block 2w + j, tile w, j = 0 gate / 1 up; lane
+ *   l = 16*c + col holds gu_q row j*I + 16*(11*cb + w) + col, bytes
+ *   64*g + 16*c .. +16), then nt*128 bytes (tile w, column col: gate scale,
+ *   gate zero, up scale, up zero of group g, fp16).
+ *   ksl_moe_pack_gateup_bytes(E, H, I) = E*H*I*17/16 bytes.
+ * H % 128 == 0, I % 64 == 0, H, I <= 8192. gu_* as ksl_moe_w4a16_forward. */
+size_t ksl_moe_pack_gateup_bytes(int64_t E, int64_t H, int64_t I);
+int ksl_moe_pack_gateup(const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H, int64_t I,
+                        uint8_t* gu_pack, void* stream);
+
+/* Down: per expert e, unit q (352 columns of H; nt = min(22, H/16 - 22*q)
+ * tiles), slot s < I/128: nt blocks of 1 KB (tile u; lane l = 16*c + col
+ * holds dn_q row 16*(22*q + u) + col, bytes 64*s + 16*c .. +16), then nt*128
+ * bytes (tile u, column col: scale and zero of group 2s, then of group
+ * 2s + 1); for I % 128 == 64 a tail slot: nt blocks of 512 B (lane l: bytes
+ * 64*(I/128) + 8*c .. +8), then nt*64 bytes (scale and zero of the last group).
+ * ksl_moe_pack_down_bytes(E, H, I) = E*H*I*9/16 bytes. dn_q in dn_layout
+ * (reference or tiled). */
+size_t ksl_moe_pack_down_bytes(int64_t E, int64_t H, int64_t I);
+int ksl_moe_pack_down(const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout, int64_t E, int64_t H,
+                      int64_t I, uint8_t* dn_pack, void* stream);
+
 /* Fixed-order top-k combine, no atomics: y[t,:] = fma-chain over k=0..topk-1
  * of fp32(w[t,k]) * fp32(out3[inv[t*topk+k], :]), rounded once to y_dtype.
  * Replaces _combine_kernel / _combine (kernels/fused_moe_w4_v2.py:248-288).
@@ -230,13 +287,14 @@ int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_
  * (hidden_states_flat), bf16 [T, H];
  *   moe = experts(rmsnorm(x) * pre_norm_w, topk_ids, topk_w)   as ksl_moe_layer_forward
  *   y   = the tail of ksl_moe_combine_post with residual = x.
- * Same workspace as ksl_moe_w4a16_forward; same contracts as
- * ksl_moe_layer_forward (H <= 4096) and ksl_moe_combine_post. Not a
- * reference entry point (see ksl_moe_combine_post). */
+ * Same workspace and weight arguments as ksl_moe_w4a16_forward; same
+ * contracts as ksl_moe_layer_forward (H <= 4096) and ksl_moe_combine_post.
+ * Not a reference entry point (see ksl_moe_combine_post). */
 int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
                           const int64_t* topk_ids, const void* topk_w, int w_dtype,
                           const uint8_t* gu_q, const void* gu_s, const void* gu_z,
-                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout, int64_t T,
+                          const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                          const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t T,
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, const void* h1,
                           int64_t h1_stride, const void* post2_w, float post2_eps, const void* post_w,
                           float post_eps, const void* layer_scalar, int ls_dtype, void* y,

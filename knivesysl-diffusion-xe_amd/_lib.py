@@ -36,23 +36,29 @@ SIGNATURES = {
     "ksl_rmsnorm": ([_P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _F, _P], _I),
     "ksl_moe_align": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
-    "ksl_moe_w4a16_forward": ([_P, _I, _I64, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
+    "ksl_moe_w4a16_forward": ([_P, _I, _I64, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _I64, _P, _P], _I),
     "ksl_moe_gateup_act": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P], _I),
     "ksl_moe_down": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I, _P], _I),
     "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
-    "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
+    "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P, _SZ, _P], _I),
     "ksl_moe_route_scratch_bytes": ([_I64, _I64, _I64], _SZ),
     "ksl_moe_router": ([_P, _I, _I64, _P, _P, _P, _I, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_combine_post": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _P, _F,
                               _P, _I, _P, _I64, _P], _I),
-    "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I,
+    "ksl_moe_block_forward": ([_P, _I64, _P, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _F, _P, _F, _P, _I,
                                _P, _I64, _P, _SZ, _P], _I),
+    "ksl_moe_ffn_ctl_bytes": ([_I64], _SZ),
+    "ksl_moe_ffn": ([_P, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P, _P], _I),
+    "ksl_moe_pack_gateup_bytes": ([_I64, _I64, _I64], _SZ),
+    "ksl_moe_pack_gateup": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_moe_pack_down_bytes": ([_I64, _I64, _I64], _SZ),
+    "ksl_moe_pack_down": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _P], _I),
     "ksl_entropy": ([_P, _I, _I64, _I64, _I64, _P, _P], _I),
     "ksl_gumbel_argmax": ([_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P], _I),
     "ksl_sample_step": ([_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),

@@ -19,6 +19,10 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 
+// Words between two counters of the one-launch expert FFN's ctl array (256
+// bytes: no two counters share a cache line); the routing launch clears them.
+constexpr int kCtlStride = 64;
+
 // ---- scalar conversions -----------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
@@ -295,6 +299,82 @@ __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__
         for (int j = 0; j < 8; ++j) o[j] = rms_apply<HAS_W>(xf[j], r, HAS_W ? wf[j] : 1.0f);
         emit(s, c0, o);
     }
+}
+
+
+// ---- expert GEMM helpers shared by the kernels of moe_gemm.hip and moe_ffn.hip
+
+template <int ACT>
+__device__ __forceinline__ float act_times_up(float g, float u) {
+    if (ACT == KSL_ACT_GELU_TANH) {
+        // kernels/fused_moe_w4_v2.py:136-138
+        const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+        const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
+        return 0.5f * g * (1.0f + th) * u;
+    } else {
+        return g / (1.0f + expf(-g)) * u;
+    }
+}
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* gbl_vptr;
+
+// Direct global -> LDS copy of one fragment block: lane L's 16 bytes land at
+// lds_block + 16*L. lds_block must be wave-uniform. Completion is tracked by
+// the issuing wave's vmcnt only.
+__device__ __forceinline__ void dma16(const void* src, char* lds_block) {
+    __builtin_amdgcn_global_load_lds((gbl_vptr)(const_cast<void*>(src)), (lds_vptr)lds_block, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N), other counters left free (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most n groups of k loads each are outstanding, n in [0, NMAX].
+template <int K, int NMAX>
+__device__ __forceinline__ void vm_wait_groups(int n) {
+    if constexpr (NMAX > 0) {
+        if (n >= NMAX) {
+            vm_wait<NMAX * K>();
+            return;
+        }
+        vm_wait_groups<K, NMAX - 1>(n);
+    } else {
+        vm_wait<0>();
+    }
+}
+
+// Workgroup barrier of a wave whose only LDS writes are direct global->LDS
+// loads that it has already waited for with vm_wait. __syncthreads() would
+// add s_waitcnt vmcnt(0) for the still-pending loads of later groups and
+// drain the ring; the asm statements keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void dma_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// LDS position (16-byte unit) of MFMA lane (row, k-group c) within a fragment
+// block of 16 rows x 64 bytes. Blocks are fetched row-major (4 consecutive
+// lanes per 64-byte row: whole 64-byte segments per 4 lanes, which streams
+// faster than 16 rows per 4 lanes), and chunk c of row r sits at
+// r*4 + (c ^ swz(r)), swz(r) = (r/2 ^ 3*(r/8)) % 4, so that the 16 lanes of
+// one k-group cover all 64 four-byte banks and each 8 of them (rows 0-7,
+// 8-15) 32 distinct banks modulo 32.
+__device__ __forceinline__ int frag_swz(int row) { return ((row >> 1) ^ (row >> 3) * 3) & 3; }
+__device__ __forceinline__ int frag_pos(int row, int c) { return row * 4 + (c ^ frag_swz(row)); }
+constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
+
+// Workgroup barrier after this wave's LDS reads (no wait on global memory).
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 }  // namespace ksl

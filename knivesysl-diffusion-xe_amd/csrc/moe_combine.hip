@@ -11,12 +11,20 @@ namespace ksl {
 
 // bcnt: workspace for the per-block counts of the multi-block routing
 // (ceil(T*topk / 1024) * E int32), or null for the single-workgroup routing.
+// zero: nzero int32 words the routing launch clears (the expert FFN's
+// counters), or null.
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
-                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st);
+                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st, int32_t* zero, int nzero);
 int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
-               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st);
+               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st, int32_t* zero, int nzero);
+// the fused expert FFN (moe_ffn.hip)
+size_t ffn_ctl_words(int64_t E);
+bool ffn_supported(int64_t E, int64_t H, int64_t I, int64_t nrows);
+int launch_ffn(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
+               const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t E, int64_t H, int64_t I, int act,
+               void* out2, void* out3, int32_t* ctl, int64_t nrows, hipStream_t st);
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
                   const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H,
                   int64_t I, int act, void* out2, hipStream_t st, int64_t nrows_hint);
@@ -269,9 +277,10 @@ int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int
 // Workspace layout of the fused forward (each region 256-byte aligned):
 //   sorted_rows i32[Nexp] | offsets i32[E+1] | inv i32[Nexp] |
 //   a16 f16[T*H] | out2 f16[Nexp*I] | out3 f16[Nexp*H] |
-//   bcnt i32[ceil(Nexp/1024) * E] (per-block expert counts of the multi-block routing)
+//   bcnt i32[ceil(Nexp/1024) * E] (per-block expert counts of the multi-block routing) |
+//   ctl i32[E+2] (the one-launch expert FFN's completion counters, unit queue and error word)
 struct MoeWorkspace {
-    size_t sorted_rows, offsets, inv, a16, out2, out3, bcnt, total;
+    size_t sorted_rows, offsets, inv, a16, out2, out3, bcnt, ctl, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -287,8 +296,29 @@ static MoeWorkspace moe_workspace_layout(int64_t T, int64_t topk, int64_t E, int
     w.out2 = off;        off += align256(nexp * static_cast<size_t>(I) * 2);
     w.out3 = off;        off += align256(nexp * static_cast<size_t>(H) * 2);
     w.bcnt = off;        off += align256((nexp + 1023) / 1024 * static_cast<size_t>(E) * 4);
+    w.ctl = off;         off += align256(ffn_ctl_words(E) * 4);
     w.total = off;
     return w;
+}
+
+// The experts between routing and combine: the one-launch FFN over the pack
+// layout when the pack buffers are given and the routing is small, else the
+// gate/up and down launches over the reference (or tiled) layout.
+static int run_experts(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
+                       const uint8_t* gu_q, const void* gu_s, const void* gu_z, const uint8_t* dn_q,
+                       const void* dn_s, const void* dn_z, int dn_layout, const uint8_t* gu_pack,
+                       const uint8_t* dn_pack, int64_t E, int64_t H, int64_t I, int act, void* out2, void* out3,
+                       int32_t* ctl, int64_t nrows, hipStream_t st) {
+    if (gu_pack && dn_pack && ffn_supported(E, H, I, nrows))
+        return launch_ffn(a16, sorted_rows, offsets, topk, gu_pack, dn_pack, E, H, I, act, out2, out3, ctl, nrows,
+                          st);
+    int rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, nrows);
+    if (rc) return rc;
+    return launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, nrows);
+}
+
+static bool use_ffn(const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t E, int64_t H, int64_t I, int64_t nrows) {
+    return gu_pack && dn_pack && ffn_supported(E, H, I, nrows);
 }
 
 }  // namespace ksl
@@ -320,6 +350,7 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
                                      const int64_t* topk_ids, const void* topk_w, int w_dtype,
                                      const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                                      const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                                     const uint8_t* gu_pack, const uint8_t* dn_pack,
                                      int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
                                      void* y, int y_dtype, int64_t y_stride, void* workspace,
                                      size_t workspace_bytes, void* stream) {
@@ -340,13 +371,14 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
     int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
+    int32_t* ctl = reinterpret_cast<int32_t*>(ws + L.ctl);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool ffn = use_ffn(gu_pack, dn_pack, E, H, I, T * topk);
     int rc = route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
-                           hidden_stride, H, a16, bcnt, st);
+                           hidden_stride, H, a16, bcnt, st, ffn ? ctl : nullptr, static_cast<int>(ffn_ctl_words(E) / kCtlStride));
     if (rc) return rc;
-    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
-    if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
+    rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
+                     E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -355,7 +387,8 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
                                      int norm_w_dtype, float eps, const int64_t* topk_ids,
                                      const void* topk_w, int w_dtype, const uint8_t* gu_q,
                                      const void* gu_s, const void* gu_z, const uint8_t* dn_q,
-                                     const void* dn_s, const void* dn_z, int dn_layout, int64_t T, int64_t topk,
+                                     const void* dn_s, const void* dn_z, int dn_layout, const uint8_t* gu_pack,
+                                     const uint8_t* dn_pack, int64_t T, int64_t topk,
                                      int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                                      int64_t y_stride, void* workspace, size_t workspace_bytes,
                                      void* stream) {
@@ -376,13 +409,14 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
     int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
+    int32_t* ctl = reinterpret_cast<int32_t*>(ws + L.ctl);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool ffn = use_ffn(gu_pack, dn_pack, E, H, I, T * topk);
     int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
-                        norm_w_dtype, eps, H, a16, bcnt, st);
+                        norm_w_dtype, eps, H, a16, bcnt, st, ffn ? ctl : nullptr, static_cast<int>(ffn_ctl_words(E) / kCtlStride));
     if (rc) return rc;
-    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
-    if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
+    rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
+                     E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
@@ -391,6 +425,7 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
                                      const int64_t* topk_ids, const void* topk_w, int w_dtype,
                                      const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                                      const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                                     const uint8_t* gu_pack, const uint8_t* dn_pack,
                                      int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act,
                                      const void* h1,
                                      int64_t h1_stride, const void* post2_w, float post2_eps,
@@ -416,13 +451,14 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
     void* out2 = ws + L.out2;
     void* out3 = ws + L.out3;
     int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
+    int32_t* ctl = reinterpret_cast<int32_t*>(ws + L.ctl);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool ffn = use_ffn(gu_pack, dn_pack, E, H, I, T * topk);
     rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, KSL_DTYPE_BF16, x_stride, pre_norm_w,
-                    KSL_DTYPE_BF16, pre_eps, H, a16, bcnt, st);
+                    KSL_DTYPE_BF16, pre_eps, H, a16, bcnt, st, ffn ? ctl : nullptr, static_cast<int>(ffn_ctl_words(E) / kCtlStride));
     if (rc) return rc;
-    rc = launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st, T * topk);
-    if (rc) return rc;
-    rc = launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, dn_layout, T * topk);
+    rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
+                     E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
     return launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, x, x_stride, post2_w,
                                post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);
@@ -444,10 +480,10 @@ extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t t
                         ? static_cast<int32_t*>(scratch)
                         : nullptr;
     return ksl::route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
-                           norm_w_dtype, eps, H, a16, bcnt, static_cast<hipStream_t>(stream));
+                           norm_w_dtype, eps, H, a16, bcnt, static_cast<hipStream_t>(stream), nullptr, 0);
 }
 
-extern "C" int ksl_version(void) { return 3; }
+extern "C" int ksl_version(void) { return 4; }
 
 extern "C" const char* ksl_status_string(int status) {
     switch (status) {

@@ -108,17 +108,6 @@ __device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offse
 }
 
 
-template <int ACT>
-__device__ __forceinline__ float act_times_up(float g, float u) {
-    if (ACT == KSL_ACT_GELU_TANH) {
-        // kernels/fused_moe_w4_v2.py:136-138
-        const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-        const float th = 2.0f / (1.0f + expf(-2.0f * inner)) - 1.0f;
-        return 0.5f * g * (1.0f + th) * u;
-    } else {
-        return g / (1.0f + expf(-g)) * u;
-    }
-}
 
 // ---------------------------------------------------------------- gate / up
 // One workgroup covers NC*16 columns of I of one expert (NC = 11: 176 columns,
@@ -135,62 +124,10 @@ __device__ __forceinline__ float act_times_up(float g, float u) {
 // workgroups keep the activation re-reads small (every requested byte costs
 // load bandwidth, L2 hit or not): the gathered rows of an expert are read
 // I/(16*NC) times per layer instead of once per 64-column block.
-typedef __attribute__((address_space(3))) void* lds_vptr;
-typedef __attribute__((address_space(1))) void* gbl_vptr;
-
-// Direct global -> LDS copy of one fragment block: lane L's 16 bytes land at
-// lds_block + 16*L. lds_block must be wave-uniform. Completion is tracked by
-// the issuing wave's vmcnt only.
-__device__ __forceinline__ void dma16(const void* src, char* lds_block) {
-    __builtin_amdgcn_global_load_lds((gbl_vptr)(const_cast<void*>(src)), (lds_vptr)lds_block, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N), other counters left free (gfx9 encoding: vmcnt bits
-// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Wait until at most n groups of k loads each are outstanding, n in [0, NMAX].
-template <int K, int NMAX>
-__device__ __forceinline__ void vm_wait_groups(int n) {
-    if constexpr (NMAX > 0) {
-        if (n >= NMAX) {
-            vm_wait<NMAX * K>();
-            return;
-        }
-        vm_wait_groups<K, NMAX - 1>(n);
-    } else {
-        vm_wait<0>();
-    }
-}
-
-// Workgroup barrier of a wave whose only LDS writes are direct global->LDS
-// loads that it has already waited for with vm_wait. __syncthreads() would
-// add s_waitcnt vmcnt(0) for the still-pending loads of later groups and
-// drain the ring; the asm statements keep the compiler from moving memory
-// operations across the barrier.
-__device__ __forceinline__ void dma_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
 
-// LDS position (16-byte unit) of MFMA lane (row, k-group c) within a fragment
-// block of 16 rows x 64 bytes. Blocks are fetched row-major (4 consecutive
-// lanes per 64-byte row: whole 64-byte segments per 4 lanes, which streams
-// faster than 16 rows per 4 lanes), and chunk c of row r sits at
-// r*4 + (c ^ swz(r)), swz(r) = (r/2 ^ 3*(r/8)) % 4, so that the 16 lanes of
-// one k-group cover all 64 four-byte banks and each 8 of them (rows 0-7,
-// 8-15) 32 distinct banks modulo 32.
-__device__ __forceinline__ int frag_swz(int row) { return ((row >> 1) ^ (row >> 3) * 3) & 3; }
-__device__ __forceinline__ int frag_pos(int row, int c) { return row * 4 + (c ^ frag_swz(row)); }
 constexpr size_t kLdsBytes = 160 * 1024;         // LDS per workgroup on gfx950
-constexpr int kBlk = kWave * 16;                 // one fragment block: 64 lanes x 16 B
 constexpr int kGuMaxG = 32;                      // H <= 4096
 
 struct GuArgs {
@@ -797,12 +734,6 @@ __device__ __forceinline__ void dn_stage_a(const DnArgs& A, char* a_lds, int sta
     }
 }
 
-// Workgroup barrier after this wave's LDS reads (no wait on global memory).
-__device__ __forceinline__ void lds_sync() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 // Buffer resource over `bytes` bytes at p (gfx9 raw buffer: stride 0, byte
 // offsets; a store at an offset past the end is dropped by the hardware).

@@ -75,7 +75,15 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* lds_wave, int64_t* t
 struct RouteOut {
     int64_t Nexp, cap, max_blocks, block_m;
     int E;
+    int32_t* zero;  // counters cleared by the routing (the expert FFN's), kCtlStride words apart, or null
+    int nzero;
 };
+
+// Clear the n counters (kCtlStride words apart) a following launch expects
+// to be zero (the one-launch expert FFN's unit queue and completion counts).
+__device__ __forceinline__ void clear_words(int32_t* __restrict__ p, int n, int t, int nt) {
+    for (int i = t; i < n; i += nt) p[static_cast<int64_t>(i) * kCtlStride] = 0;
+}
 
 template <typename IdxT>
 __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, IdxT* __restrict__ sorted_rows,
@@ -112,7 +120,7 @@ constexpr int kFastPer = kFastPad / (kFastWaves * kWave); // ids loaded per thre
 // offsets[E] and the unused tail slots (Nexp).
 __device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, int Nexp, int E,
                                               int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv,
-                                              int32_t* __restrict__ offsets) {
+                                              int32_t* __restrict__ offsets, int32_t* __restrict__ zero, int nzero) {
     __shared__ __attribute__((aligned(16))) uint16_t keys[kFastPad];
     const int lane = threadIdx.x & (kWave - 1);
     const int e = blockIdx.x * kFastWaves + threadIdx.x / kWave;
@@ -181,8 +189,10 @@ __device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, i
         }
     }
     if (lane == 0) offsets[e] = before;
-    if (e == E)
+    if (e == E) {
         for (int p = before + lane; p < Nexp; p += kWave) sorted_rows[p] = Nexp;
+        if (zero) clear_words(zero, nzero, lane, kWave);
+    }
 }
 
 // Activation prep by workgroup blk of nblk: hidden -> fp16, 8-blocks in K-slot order.
@@ -261,11 +271,11 @@ template <int HD>
 __global__ __launch_bounds__(kFastWaves * kWave) void route_fast_kernel(
     const int64_t* __restrict__ ids, int Nexp, int E, int nrw, int32_t* __restrict__ sorted_rows,
     int32_t* __restrict__ inv, int32_t* __restrict__ offsets, const void* __restrict__ hidden,
-    int64_t hidden_stride, int64_t T, int64_t H, f16* __restrict__ a16) {
+    int64_t hidden_stride, int64_t T, int64_t H, f16* __restrict__ a16, int32_t* __restrict__ zero, int nzero) {
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     if (static_cast<int>(blockIdx.x) < nrw) {
-        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets);
+        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets, zero, nzero);
         return;
     }
     const int64_t row = static_cast<int64_t>(blockIdx.x - nrw) * kFastWaves + wave;
@@ -285,11 +295,12 @@ template <int XD, int WD, int NSTEP, bool HAS_W>
 __global__ __launch_bounds__(kFastWaves * kWave) void route_norm_fast_kernel(
     const int64_t* __restrict__ ids, int Nexp, int E, int nrw, int32_t* __restrict__ sorted_rows,
     int32_t* __restrict__ inv, int32_t* __restrict__ offsets, const void* __restrict__ xv, int64_t x_stride,
-    const void* __restrict__ wv, float eps, int64_t T, int64_t H, f16* __restrict__ a16) {
+    const void* __restrict__ wv, float eps, int64_t T, int64_t H, f16* __restrict__ a16, int32_t* __restrict__ zero,
+    int nzero) {
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     if (static_cast<int>(blockIdx.x) < nrw) {
-        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets);
+        route_fast_wg(ids, Nexp, E, sorted_rows, inv, offsets, zero, nzero);
         return;
     }
     const int64_t row = static_cast<int64_t>(blockIdx.x - nrw) * kFastWaves + wave;
@@ -390,6 +401,7 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
         if (offsets) offsets[e] = static_cast<int32_t>(blk_start * block_m);
     }
     if (offsets && threadIdx.x == 0) offsets[E] = static_cast<int32_t>(tot_blocks * block_m);
+    if (R.zero) clear_words(R.zero, R.nzero, threadIdx.x, kRouteThreads);
     if (sorted_rows) {
         for (int64_t p = tot_blocks * block_m + threadIdx.x; p < cap; p += kRouteThreads)
             sorted_rows[p] = static_cast<IdxT>(Nexp);
@@ -485,7 +497,8 @@ __device__ void route_mb_count(const int64_t* __restrict__ ids, int64_t Nexp, in
 
 __global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
     const int64_t* __restrict__ ids, int64_t Nexp, int E, int nb, const int32_t* __restrict__ bcnt,
-    int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv, int32_t* __restrict__ offsets) {
+    int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ zero, int nzero) {
     extern __shared__ int32_t lds[];
     int32_t* wcnt = lds;                                                  // [kRouteWaves][E]
     int64_t* estart = reinterpret_cast<int64_t*>(lds + kRouteWaves * E);  // [E]
@@ -524,6 +537,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_mb_scatter_kernel(
         if (e < E) offsets[e] = static_cast<int32_t>(start);
         if (threadIdx.x == 0) offsets[E] = static_cast<int32_t>(*total);
         for (int64_t p = *total + threadIdx.x; p < Nexp; p += kRouteThreads) sorted_rows[p] = static_cast<int32_t>(Nexp);
+        if (zero) clear_words(zero, nzero, threadIdx.x, kRouteThreads);
     }
     __syncthreads();
     int32_t* mycnt = wcnt + wave * E;
@@ -578,7 +592,7 @@ template <typename IdxT, int HD>
 int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
                  IdxT* sorted_rows, int64_t cap, IdxT* expert_ids, int64_t max_blocks, IdxT* inv,
                  int32_t* offsets, const void* hidden, int64_t hstride, int64_t H, f16* a16,
-                 hipStream_t st) {
+                 hipStream_t st, int32_t* zero = nullptr, int nzero = 0) {
     const int64_t Nexp = T * topk;
     unsigned grid = 1;
     if (a16) {
@@ -589,7 +603,7 @@ int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t
         grid += static_cast<unsigned>(want);
     }
     const size_t lds_bytes = route_lds_bytes(E);
-    RouteOut R{Nexp, cap, max_blocks, block_m, static_cast<int>(E)};
+    RouteOut R{Nexp, cap, max_blocks, block_m, static_cast<int>(E), zero, nzero};
     hipLaunchKernelGGL((route_kernel<IdxT, HD>), dim3(grid), dim3(kRouteThreads), lds_bytes, st, ids, R,
                        sorted_rows, expert_ids, inv, offsets, hidden, hstride, T, H, a16);
     KSL_LAUNCH_CHECK();
@@ -617,7 +631,7 @@ extern "C" int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, i
 namespace ksl {
 int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                   int32_t* offsets, int32_t* inv, const void* hidden, int hd, int64_t hstride,
-                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st) {
+                  int64_t H, void* a16, int32_t* bcnt, hipStream_t st, int32_t* zero, int nzero) {
     if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
     if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     if (T > 0 && !ids) return KSL_ERR_ARG;
@@ -635,15 +649,15 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
         switch (hd) {
             case KSL_DTYPE_BF16:
                 hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_BF16>, grid, block, 0, st, ids, static_cast<int>(Nexp),
-                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a, zero, nzero);
                 break;
             case KSL_DTYPE_F16:
                 hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_F16>, grid, block, 0, st, ids, static_cast<int>(Nexp),
-                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a, zero, nzero);
                 break;
             case KSL_DTYPE_F32:
                 hipLaunchKernelGGL(route_fast_kernel<KSL_DTYPE_F32>, grid, block, 0, st, ids, static_cast<int>(Nexp),
-                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a);
+                                   static_cast<int>(E), nrw, sorted_rows, inv, offsets, hidden, hstride, T, H, a, zero, nzero);
                 break;
             default:
                 return KSL_ERR_ARG;
@@ -680,7 +694,7 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
         }
         KSL_LAUNCH_CHECK();
         hipLaunchKernelGGL(route_mb_scatter_kernel, dim3(nb), block, lds, st, ids, Nexp, e, nb, bcnt, sorted_rows, inv,
-                           offsets);
+                           offsets, zero, nzero);
         KSL_LAUNCH_CHECK();
         return KSL_OK;
     }
@@ -689,13 +703,13 @@ int route_compact(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_
     switch (hd) {
         case KSL_DTYPE_BF16:
             return launch_route<int32_t, KSL_DTYPE_BF16>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
-                                                         inv, offsets, hidden, hstride, H, a, st);
+                                                         inv, offsets, hidden, hstride, H, a, st, zero, nzero);
         case KSL_DTYPE_F16:
             return launch_route<int32_t, KSL_DTYPE_F16>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
-                                                        inv, offsets, hidden, hstride, H, a, st);
+                                                        inv, offsets, hidden, hstride, H, a, st, zero, nzero);
         case KSL_DTYPE_F32:
             return launch_route<int32_t, KSL_DTYPE_F32>(ids, T, topk, E, 1, sorted_rows, Nexp, nullptr, 0,
-                                                        inv, offsets, hidden, hstride, H, a, st);
+                                                        inv, offsets, hidden, hstride, H, a, st, zero, nzero);
     }
     return KSL_ERR_ARG;
 }
@@ -713,7 +727,7 @@ int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32
         const int nexp = static_cast<int>(R.Nexp);
 #define KSL_RNF(NS)                                                                                          \
     hipLaunchKernelGGL((route_norm_fast_kernel<XD, WD, NS, HAS_W>), fgrid, fblock, 0, st, ids, nexp, R.E, nrw, \
-                       sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16)
+                       sorted_rows, inv, offsets, x, xs, w, eps, T, H, a16, R.zero, R.nzero)
         if (nstep <= 1) KSL_RNF(1);
         else if (nstep <= 2) KSL_RNF(2);
         else if (nstep <= 4) KSL_RNF(4);
@@ -742,7 +756,7 @@ int launch_route_norm_ns(int nstep, const int64_t* ids, const RouteOut& R, int32
 #undef KSL_RNM
         KSL_LAUNCH_CHECK();
         hipLaunchKernelGGL(route_mb_scatter_kernel, dim3(nb), dim3(kRouteThreads), lds, st, ids, R.Nexp, R.E, nb, bcnt,
-                           sorted_rows, inv, offsets);
+                           sorted_rows, inv, offsets, R.zero, R.nzero);
         KSL_LAUNCH_CHECK();
         return KSL_OK;
     }
@@ -776,7 +790,7 @@ int launch_route_norm_x(int wd, int nstep, const int64_t* ids, const RouteOut& R
 // Routing plus RMSNorm -> fp16 activations in one launch (the layer path).
 int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_rows,
                int32_t* offsets, int32_t* inv, const void* x, int xd, int64_t xs, const void* w,
-               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st) {
+               int wd, float eps, int64_t H, void* a16, int32_t* bcnt, hipStream_t st, int32_t* zero, int nzero) {
     if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts) return KSL_ERR_SHAPE;
     if (T * topk >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     if (H <= 0 || H % 128 != 0 || H > 4096 || xs < H || xs % 8 != 0) return KSL_ERR_SHAPE;
@@ -785,7 +799,7 @@ int route_norm(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int32_t* 
         (w && reinterpret_cast<uintptr_t>(w) % 16))
         return KSL_ERR_ALIGN;
     const int64_t Nexp = T * topk;
-    RouteOut R{Nexp, Nexp, 0, 1, static_cast<int>(E)};
+    RouteOut R{Nexp, Nexp, 0, 1, static_cast<int>(E), zero, nzero};
     const int nstep = static_cast<int>((H / 8 + kWave - 1) / kWave);
     f16* a = static_cast<f16*>(a16);
     switch (xd) {
@@ -801,5 +815,5 @@ extern "C" int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, i
                              const void* hidden, int hidden_dtype, int64_t hidden_stride, int64_t H,
                              void* a16, void* stream) {
     return ksl::route_compact(topk_ids, T, topk, E, sorted_rows, offsets, inv, hidden, hidden_dtype,
-                              hidden_stride, H, a16, nullptr, static_cast<hipStream_t>(stream));
+                              hidden_stride, H, a16, nullptr, static_cast<hipStream_t>(stream), nullptr, 0);
 }

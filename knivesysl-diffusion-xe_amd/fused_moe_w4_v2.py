@@ -150,6 +150,49 @@ def enable_tiled_down(exp, cache: dict | None = None):
     return exp
 
 
+@torch.no_grad()
+def pack_weights(exp) -> tuple[torch.Tensor, torch.Tensor]:
+    """The experts' gate/up and down weights in the pack layout of the
+    one-launch expert FFN (ksl_moe_pack_gateup / ksl_moe_pack_down): new
+    uint8 tensors holding the same nibbles, scales and zero-points."""
+    E, twoI, Hh = exp.gu_q.shape
+    H, I = 2 * Hh, twoI // 2
+    _check_weights(exp, E, H, I)
+    lib = _lib.load()
+    st = _lib.stream_of(exp.gu_q)
+    gu = torch.empty(int(lib.ksl_moe_pack_gateup_bytes(E, H, I)), dtype=torch.uint8, device=exp.gu_q.device)
+    dn = torch.empty(int(lib.ksl_moe_pack_down_bytes(E, H, I)), dtype=torch.uint8, device=exp.gu_q.device)
+    _lib.check(lib.ksl_moe_pack_gateup(_lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z), E, H, I,
+                                       _lib.ptr(gu), st), "ksl_moe_pack_gateup")
+    _lib.check(lib.ksl_moe_pack_down(_lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp),
+                                     E, H, I, _lib.ptr(dn), st), "ksl_moe_pack_down")
+    return gu, dn
+
+
+def enable_pack(exp, cache: dict | None = None):
+    """Give exp the pack layout (exp.gu_pack, exp.dn_pack), with which the
+    forwards of this package run gate/up and down as one launch for routings
+    of at most 8192 rows (same results). The reference buffers stay for larger
+    routings. Idempotent; `cache` keeps modules that share their buffers (the
+    encoder and decoder experts of a layer, kernels/load_w4_checkpoint.py:56-59)
+    sharing one pack."""
+    if getattr(exp, "gu_pack", None) is not None and getattr(exp, "dn_pack", None) is not None:
+        return exp
+    key = (exp.gu_q.data_ptr(), exp.dn_q.data_ptr(), str(exp.gu_q.device))
+    t = None if cache is None else cache.get(key)
+    if t is None:
+        t = pack_weights(exp)
+        if cache is not None:
+            cache[key] = t
+    exp.gu_pack, exp.dn_pack = t
+    return exp
+
+
+def pack_ptrs(exp):
+    """(gu_pack, dn_pack) device pointers for the C forwards (NULL without a pack)."""
+    return _lib.ptr(getattr(exp, "gu_pack", None)), _lib.ptr(getattr(exp, "dn_pack", None))
+
+
 def moe_workspace(T: int, tk: int, E: int, H: int, I: int, device) -> torch.Tensor:
     nbytes = int(_lib.load().ksl_moe_workspace_bytes(T, tk, E, H, I))
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -189,7 +232,7 @@ def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: t
         _lib.ptr(hidden), _lib.dtype_code(hidden.dtype), hidden.stride(0),
         _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
         _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
-        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp), *pack_ptrs(exp),
         T, tk, E, K, I, exp._ksl_act,
         _lib.ptr(y), _lib.dtype_code(y_dtype), y.stride(0),
         _lib.ptr(workspace), workspace.numel(), _lib.stream_of(hidden))

@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fused_moe_w4_v2 import _check_act, _check_weights, dn_layout, moe_workspace
+from .fused_moe_w4_v2 import _check_act, _check_weights, dn_layout, moe_workspace, pack_ptrs
 
 
 def _rows(t: torch.Tensor, H: int) -> torch.Tensor:
@@ -90,7 +90,7 @@ def moe_block_forward(layer, residual: torch.Tensor, hidden_states_1: torch.Tens
         _lib.ptr(x), x.stride(0), _lib.ptr(pre_w), float(pre.eps),
         _lib.ptr(ids), _lib.ptr(w), _lib.dtype_code(w.dtype),
         _lib.ptr(exp.gu_q), _lib.ptr(exp.gu_s), _lib.ptr(exp.gu_z),
-        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp),
+        _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s), _lib.ptr(exp.dn_z), dn_layout(exp), *pack_ptrs(exp),
         T, tk, E, H, I, exp._ksl_act,
         _lib.ptr(h1), h1.stride(0), _lib.ptr(post2_w), float(post2.eps), _lib.ptr(post_w), float(post.eps),
         _lib.ptr(ls), _lib.DTYPE_BF16 if ls is None else _lib.dtype_code(ls.dtype),

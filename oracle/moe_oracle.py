@@ -161,6 +161,78 @@ def untile_down(tiled: np.ndarray, I: int) -> np.ndarray:
     return out
 
 
+def unpack_gateup(pack: np.ndarray, E: int, H: int, I: int):
+    """Read the gate/up pack layout of the one-launch expert FFN back into the
+    reference buffers (gu_q [E, 2I, H/2] uint8, gu_s / gu_z [E, 2I, H/128]
+    fp16). The pack is this build's load-time repack (the reference's
+    precedent: kernels/fused_moe_w4_v2.py:187-206). Per expert, unit cb
+    (nt = min(11, I/16 - 11 cb) tiles of 16 columns of I), group g: nt*2 blocks
+    of 1 KB (block 2w + j, tile w, j = 0 gate / 1 up; lane l = 16 c + col
+    holds row j*I + 16 (11 cb + w) + col, bytes 64 g + 16 c .. +16), then
+    nt*128 bytes (tile w, column col: s_gate, z_gate, s_up, z_up, fp16)."""
+    G = H // 128
+    pk = pack.reshape(E, -1)
+    q = np.zeros((E, 2 * I, H // 2), np.uint8)
+    sc = np.zeros((E, 2 * I, G), np.float16)
+    zp = np.zeros((E, 2 * I, G), np.float16)
+    off = 0
+    for cb in range((I // 16 + 10) // 11):
+        nt = min(11, I // 16 - 11 * cb)
+        for g in range(G):
+            blocks = pk[:, off:off + nt * 2048].reshape(E, nt, 2, 4, 16, 16)   # [e, w, j, c, col, byte]
+            sz = pk[:, off + nt * 2048:off + nt * 2176].copy().view(np.float16).reshape(E, nt, 16, 4)
+            for w in range(nt):
+                for j in range(2):
+                    rows = j * I + 16 * (11 * cb + w) + np.arange(16)
+                    for c in range(4):
+                        q[:, rows, 64 * g + 16 * c:64 * g + 16 * c + 16] = blocks[:, w, j, c]
+                    sc[:, rows, g] = sz[:, w, :, 2 * j]
+                    zp[:, rows, g] = sz[:, w, :, 2 * j + 1]
+            off += nt * 2176
+    return q, sc, zp
+
+
+def unpack_down(pack: np.ndarray, E: int, H: int, I: int):
+    """Read the down pack layout back into dn_q [E, H, I/2] uint8 (reference
+    layout), dn_s / dn_z [E, H, I/64] fp16. Per expert, unit q (nt = min(22,
+    H/16 - 22 q) tiles of 16 columns of H), slot s < I/128: nt blocks of 1 KB
+    (tile u; lane l = 16 c + col holds row 16 (22 q + u) + col, bytes
+    64 s + 16 c .. +16), then nt*128 bytes (tile u, column col: s, z of group
+    2s, then of group 2s + 1); for I % 128 == 64 a tail slot: nt blocks of
+    512 B (lane l: bytes 64 (I/128) + 8 c .. +8), then nt*64 bytes (s, z of the
+    last group)."""
+    Gd, nfull = I // 64, I // 128
+    pk = pack.reshape(E, -1)
+    q = np.zeros((E, H, I // 2), np.uint8)
+    sc = np.zeros((E, H, Gd), np.float16)
+    zp = np.zeros((E, H, Gd), np.float16)
+    off = 0
+    for qb in range((H // 16 + 21) // 22):
+        nt = min(22, H // 16 - 22 * qb)
+        for sl in range(nfull):
+            blocks = pk[:, off:off + nt * 1024].reshape(E, nt, 4, 16, 16)      # [e, u, c, col, byte]
+            sz = pk[:, off + nt * 1024:off + nt * 1152].copy().view(np.float16).reshape(E, nt, 16, 2, 2)
+            for u in range(nt):
+                rows = 16 * (22 * qb + u) + np.arange(16)
+                for c in range(4):
+                    q[:, rows, 64 * sl + 16 * c:64 * sl + 16 * c + 16] = blocks[:, u, c]
+                for h in range(2):
+                    sc[:, rows, 2 * sl + h] = sz[:, u, :, h, 0]
+                    zp[:, rows, 2 * sl + h] = sz[:, u, :, h, 1]
+            off += nt * 1152
+        if I % 128:
+            blocks = pk[:, off:off + nt * 512].reshape(E, nt, 4, 16, 8)
+            sz = pk[:, off + nt * 512:off + nt * 576].copy().view(np.float16).reshape(E, nt, 16, 2)
+            for u in range(nt):
+                rows = 16 * (22 * qb + u) + np.arange(16)
+                for c in range(4):
+                    q[:, rows, 64 * nfull + 8 * c:64 * nfull + 8 * c + 8] = blocks[:, u, c]
+                sc[:, rows, Gd - 1] = sz[:, u, :, 0]
+                zp[:, rows, Gd - 1] = sz[:, u, :, 1]
+            off += nt * 576
+    return q, sc, zp
+
+
 # ----------------------------------------------------------------------------
 # Routing metadata — kernels/fused_moe_w4.py:15-51 (moe_align)
 # ----------------------------------------------------------------------------

@@ -133,7 +133,7 @@ def test_block_tail_entry_points_reject_bad_arguments_without_launching():
 
     def block(T=256, H=2816, I=704, act=1, h1=fake, ws=null, wsb=0, layout=0):
         return L.ksl_moe_block_forward(fake, H, fake, 1e-6, fake, fake, 0, fake, fake, fake, fake, fake, fake, layout,
-                                       T, 8, 128, H, I, act, h1, H, fake, 1e-6, fake, 1e-6, null, 2, fake, H,
+                                       null, null, T, 8, 128, H, I, act, h1, H, fake, 1e-6, fake, 1e-6, null, 2, fake, H,
                                        ws, wsb, null)
     assert block(I=700) == 2 and block(H=2800) == 2
     assert block(act=9) == 1

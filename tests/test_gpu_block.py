@@ -137,11 +137,12 @@ def test_block_forward_canvas_256(gpu):
     bufs_t = bufs[:3] + [lib.ptr(dn_t)] + bufs[4:]
     print("block_forward T=256 H=2816 I=704 E=128 top-8", flush=True)
     rc = L.ksl_moe_layer_forward(lib.ptr(xd), lib.DTYPE_BF16, H, lib.ptr(pre_d), lib.DTYPE_BF16, 1e-6,
-                                 lib.ptr(ids_d), lib.ptr(w_d), lib.DTYPE_F32, *bufs, lib.DN_LAYOUT_REF, T, tk, E, H, I,
+                                 lib.ptr(ids_d), lib.ptr(w_d), lib.DTYPE_F32, *bufs, lib.DN_LAYOUT_REF, None, None,
+                                 T, tk, E, H, I,
                                  lib.ACT_SILU, lib.ptr(m), lib.DTYPE_BF16, H, lib.ptr(ws), nbytes, st)
     lib.check(rc, "ksl_moe_layer_forward")
     rc = L.ksl_moe_block_forward(lib.ptr(xd), H, lib.ptr(pre_d), 1e-6, lib.ptr(ids_d), lib.ptr(w_d), lib.DTYPE_F32,
-                                 *bufs_t, lib.DN_LAYOUT_TILED, T, tk, E, H, I, lib.ACT_SILU, lib.ptr(h1_d), H,
+                                 *bufs_t, lib.DN_LAYOUT_TILED, None, None, T, tk, E, H, I, lib.ACT_SILU, lib.ptr(h1_d), H,
                                  lib.ptr(w2_d), 1e-6,
                                  lib.ptr(wp_d), 1e-6, lib.ptr(ls_d), lib.DTYPE_BF16, lib.ptr(y), H,
                                  lib.ptr(ws), nbytes, st)

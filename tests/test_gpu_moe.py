@@ -211,7 +211,7 @@ def test_fused_forward_multiblock_routing_in_workspace(gpu):
     bufs = [lib.ptr(getattr(exp, k)) for k in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z")]
     print(f"w4a16_forward multi-block routing T={T} topk={tk} E={E}", flush=True)
     rc = L.ksl_moe_w4a16_forward(lib.ptr(hg), lib.DTYPE_BF16, H, lib.ptr(idsg), lib.ptr(wg), lib.DTYPE_F32, *bufs,
-                                 lib.DN_LAYOUT_REF, T, tk, E, H, I, lib.ACT_SILU, lib.ptr(y), lib.DTYPE_BF16, H,
+                                 lib.DN_LAYOUT_REF, None, None, T, tk, E, H, I, lib.ACT_SILU, lib.ptr(y), lib.DTYPE_BF16, H,
                                  lib.ptr(ws), nbytes, st)
     lib.check(rc, "ksl_moe_w4a16_forward")
     torch.cuda.synchronize()
