@@ -28,6 +28,8 @@ extern "C" {
 #define KSL_ERR_ALIGN 3     /* pointer or stride alignment contract violated */
 #define KSL_ERR_LAUNCH 4    /* kernel launch failed */
 #define KSL_ERR_WORKSPACE 5 /* workspace too small */
+#define KSL_ERR_SCRATCH 6   /* input larger than ksl_moe_layer_forward_noalloc's scratch */
+#define KSL_ERR_RUNTIME 7   /* a HIP runtime query failed */
 
 /* storage dtype codes */
 #define KSL_DTYPE_F32 0
@@ -124,6 +126,31 @@ int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const vo
                           const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t T,
                           int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
                           int64_t y_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of the library's own per-GPU scratch array, the workspace of
+ * ksl_moe_layer_forward_noalloc: 32 MiB, enough for T * topk = 4096 routed
+ * rows at H = 2816, I = 704, E = 128 (ksl_moe_workspace_bytes gives the need
+ * of a shape). Every GPU the library runs on holds one until the process ends. */
+#define KSL_NOALLOC_SCRATCH_BYTES (32 * 1024 * 1024)
+
+/* ksl_moe_layer_forward without the workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments, contracts and results as ksl_moe_layer_forward; its
+ * workspace is a static array of KSL_NOALLOC_SCRATCH_BYTES per GPU, found on
+ * the current device (hipGetDevice) at the first call there. Returns
+ * KSL_ERR_SCRATCH, before any device work, when ksl_moe_workspace_bytes(T,
+ * topk, E, H, I) exceeds it, and KSL_ERR_RUNTIME when the array's address
+ * cannot be looked up. Allocates nothing (no hipMalloc, no library
+ * allocation). All calls on one GPU share its array: calls that overlap on
+ * one GPU (other streams, other threads) race; calls on one stream do not. */
+int ksl_moe_layer_forward_noalloc(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
+                                  int norm_w_dtype, float eps, const int64_t* topk_ids, const void* topk_w,
+                                  int w_dtype, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
+                                  const uint8_t* dn_q, const void* dn_s, const void* dn_z, int dn_layout,
+                                  const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t T,
+                                  int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y, int y_dtype,
+                                  int64_t y_stride, void* stream);
 
 /* The first stage of ksl_moe_layer_forward: compact routing (as
  * ksl_moe_route) plus a16 = fp16(bf16(rmsnorm(x) [* norm_w])) in the gate/up

@@ -17,6 +17,8 @@ LIB_PATH = os.path.join(PKG_DIR, "libksl.so")
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ACT_GELU_TANH, ACT_SILU = 0, 1
 DN_LAYOUT_REF, DN_LAYOUT_TILED = 0, 1
+ERR_SCRATCH, ERR_RUNTIME = 6, 7
+NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
 
 _TORCH_TO_CODE = {
     torch.float32: DTYPE_F32,
@@ -45,6 +47,8 @@ SIGNATURES = {
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
+    "ksl_moe_layer_forward_noalloc": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
+                                       _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P], _I),
     "ksl_moe_layer_route": ([_P, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I, _F, _I64, _P, _P, _SZ, _P], _I),
     "ksl_moe_route_scratch_bytes": ([_I64, _I64, _I64], _SZ),
     "ksl_moe_router": ([_P, _I, _I64, _P, _P, _P, _I, _F, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),

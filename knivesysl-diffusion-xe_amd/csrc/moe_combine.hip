@@ -7,6 +7,9 @@
 // token (128-bit loads of out3, 128-bit stores of y).
 #include "ksl_common.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace ksl {
 
 // bcnt: workspace for the per-block counts of the multi-block routing
@@ -383,6 +386,73 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
 }
 
+namespace ksl {
+
+// The body of ksl_moe_layer_forward after its argument checks, on the
+// workspace `ws` (laid out by moe_workspace_layout, 256-byte aligned).
+static int layer_forward_on(char* ws, const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
+                            int norm_w_dtype, float eps, const int64_t* topk_ids, const void* topk_w, int w_dtype,
+                            const uint8_t* gu_q, const void* gu_s, const void* gu_z, const uint8_t* dn_q,
+                            const void* dn_s, const void* dn_z, int dn_layout, const uint8_t* gu_pack,
+                            const uint8_t* dn_pack, int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I,
+                            int act, void* y, int y_dtype, int64_t y_stride, hipStream_t st) {
+    const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
+    int32_t* sorted_rows = reinterpret_cast<int32_t*>(ws + L.sorted_rows);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    int32_t* inv = reinterpret_cast<int32_t*>(ws + L.inv);
+    void* a16 = ws + L.a16;
+    void* out2 = ws + L.out2;
+    void* out3 = ws + L.out3;
+    int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
+    int32_t* ctl = reinterpret_cast<int32_t*>(ws + L.ctl);
+    const bool ffn = use_ffn(gu_pack, dn_pack, E, H, I, T * topk);
+    int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
+                        norm_w_dtype, eps, H, a16, bcnt, st, ffn ? ctl : nullptr, static_cast<int>(ffn_ctl_words(E) / kCtlStride));
+    if (rc) return rc;
+    rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
+                     E, H, I, act, out2, out3, ctl, T * topk, st);
+    if (rc) return rc;
+    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+}
+
+static int layer_forward_check(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act, int dn_layout) {
+    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
+    if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (dn_layout != KSL_DN_LAYOUT_REF && dn_layout != KSL_DN_LAYOUT_TILED) return KSL_ERR_ARG;
+    return KSL_OK;
+}
+
+// The library's own workspace for ksl_moe_layer_forward_noalloc: one array per
+// GPU, held from the library's load until the process ends. Host code never
+// uses the array's name as an address (on the host it is only a stand-in for
+// the symbol): scratch_on() returns the device address, looked up once per
+// device with that device current.
+static __device__ __align__(256) unsigned char scratch[KSL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<char*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array, or null on a failed lookup.
+static char* scratch_on(int dev) {
+    char* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p) return p;
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    p = static_cast<char*>(addr);
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+    return p;
+}
+
+}  // namespace ksl
+
 extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
                                      int norm_w_dtype, float eps, const int64_t* topk_ids,
                                      const void* topk_w, int w_dtype, const uint8_t* gu_q,
@@ -393,32 +463,35 @@ extern "C" int ksl_moe_layer_forward(const void* x, int x_dtype, int64_t x_strid
                                      int64_t y_stride, void* workspace, size_t workspace_bytes,
                                      void* stream) {
     using namespace ksl;
-    if (T < 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0) return KSL_ERR_SHAPE;
-    if (H % 128 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
-    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
-    if (dn_layout != KSL_DN_LAYOUT_REF && dn_layout != KSL_DN_LAYOUT_TILED) return KSL_ERR_ARG;
-    if (T == 0) return KSL_OK;
-    const MoeWorkspace L = moe_workspace_layout(T, topk, E, H, I);
-    if (!workspace || workspace_bytes < L.total) return KSL_ERR_WORKSPACE;
+    int rc = layer_forward_check(T, topk, E, H, I, act, dn_layout);
+    if (rc || T == 0) return rc;
+    if (!workspace || workspace_bytes < moe_workspace_layout(T, topk, E, H, I).total) return KSL_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % 256) return KSL_ERR_ALIGN;
-    char* ws = static_cast<char*>(workspace);
-    int32_t* sorted_rows = reinterpret_cast<int32_t*>(ws + L.sorted_rows);
-    int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
-    int32_t* inv = reinterpret_cast<int32_t*>(ws + L.inv);
-    void* a16 = ws + L.a16;
-    void* out2 = ws + L.out2;
-    void* out3 = ws + L.out3;
-    int32_t* bcnt = reinterpret_cast<int32_t*>(ws + L.bcnt);
-    int32_t* ctl = reinterpret_cast<int32_t*>(ws + L.ctl);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool ffn = use_ffn(gu_pack, dn_pack, E, H, I, T * topk);
-    int rc = route_norm(topk_ids, T, topk, E, sorted_rows, offsets, inv, x, x_dtype, x_stride, norm_w,
-                        norm_w_dtype, eps, H, a16, bcnt, st, ffn ? ctl : nullptr, static_cast<int>(ffn_ctl_words(E) / kCtlStride));
-    if (rc) return rc;
-    rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
-                     E, H, I, act, out2, out3, ctl, T * topk, st);
-    if (rc) return rc;
-    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+    return layer_forward_on(static_cast<char*>(workspace), x, x_dtype, x_stride, norm_w, norm_w_dtype, eps, topk_ids,
+                            topk_w, w_dtype, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack, T, topk,
+                            E, H, I, act, y, y_dtype, y_stride, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ksl_moe_layer_forward_noalloc(const void* x, int x_dtype, int64_t x_stride, const void* norm_w,
+                                             int norm_w_dtype, float eps, const int64_t* topk_ids,
+                                             const void* topk_w, int w_dtype, const uint8_t* gu_q,
+                                             const void* gu_s, const void* gu_z, const uint8_t* dn_q,
+                                             const void* dn_s, const void* dn_z, int dn_layout,
+                                             const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t T,
+                                             int64_t topk, int64_t E, int64_t H, int64_t I, int act, void* y,
+                                             int y_dtype, int64_t y_stride, void* stream) {
+    using namespace ksl;
+    int rc = layer_forward_check(T, topk, E, H, I, act, dn_layout);
+    if (rc || T == 0) return rc;
+    if (moe_workspace_layout(T, topk, E, H, I).total > static_cast<size_t>(KSL_NOALLOC_SCRATCH_BYTES))
+        return KSL_ERR_SCRATCH;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return KSL_ERR_RUNTIME;
+    char* ws = scratch_on(dev);
+    if (!ws) return KSL_ERR_RUNTIME;
+    return layer_forward_on(ws, x, x_dtype, x_stride, norm_w, norm_w_dtype, eps, topk_ids, topk_w, w_dtype, gu_q,
+                            gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack, T, topk, E, H, I, act, y,
+                            y_dtype, y_stride, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void* pre_norm_w, float pre_eps,
@@ -493,6 +566,8 @@ extern "C" const char* ksl_status_string(int status) {
         case KSL_ERR_ALIGN: return "pointer or stride alignment contract violated";
         case KSL_ERR_LAUNCH: return "kernel launch failed";
         case KSL_ERR_WORKSPACE: return "workspace too small";
+        case KSL_ERR_SCRATCH: return "input needs more than the no-allocation entry point's scratch (KSL_NOALLOC_SCRATCH_BYTES)";
+        case KSL_ERR_RUNTIME: return "HIP runtime call failed";
     }
     return "unknown status";
 }
