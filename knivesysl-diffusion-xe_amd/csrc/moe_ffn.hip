@@ -24,17 +24,20 @@
 // the next index from a counter. All gate/up units come before all down units,
 // chunk 0 of every expert before its later chunks.
 //
-// Waves of a workgroup (14):
+// Waves of a workgroup (15):
 //   0..10  consumers: wave w owns gate/up tile w, or down tiles 2w and 2w+1;
 //          they read LDS only (nibble decode, v_mfma_f32_16x16x32_f16) and
 //          store out2 / out3 at the end of a chunk;
-//   11     weight producer: copies each slot's contiguous pack bytes (1 KB
-//          per instruction) into the ring (direct global -> LDS loads);
-//   12     activation producer: gathers the chunk's activation rows into the
+//   11, 12 weight producers: copy the first and second half of each slot's
+//          contiguous pack bytes (1 KB per instruction) into the ring (direct
+//          global -> LDS loads);
+//   13     activation producer: gathers the chunk's activation rows into the
 //          ring in MFMA fragment order (a16 rows for gate/up, out2 rows for
 //          down);
-//   13     control: pulls units, reads the routing, tracks which experts'
+//   14     control: pulls units, reads the routing, tracks which experts'
 //          gate/up is complete, and writes one plan per ring slot into LDS.
+// Waves 11..14 run at raised priority, so that after a barrier their load
+// issue is not queued behind the consumers' arithmetic.
 // One barrier per slot. In cycle n the consumers compute slot n, the producers
 // issue slot n+R-1 and wait for slot n+1, the control wave plans slot n+R.
 // A slot whose unit cannot start yet (its expert's gate/up still running
@@ -59,10 +62,11 @@ namespace ksl {
 namespace {
 
 constexpr int kNc = 11;                 // consumer waves
-constexpr int kWaveW = kNc;             // weight producer
-constexpr int kWaveA = kNc + 1;         // activation producer
-constexpr int kWaveCtl = kNc + 2;       // control wave
-constexpr int kFfnWaves = kNc + 3;
+constexpr int kWaveW0 = kNc;            // weight producers: each slot's first and second half
+constexpr int kWaveW1 = kNc + 1;
+constexpr int kWaveA = kNc + 2;         // activation producer
+constexpr int kWaveCtl = kNc + 3;       // control wave
+constexpr int kFfnWaves = kNc + 4;
 constexpr int kFfnThreads = kFfnWaves * kWave;
 constexpr int kGuT = kNc;               // gate (and up) tiles per gate/up unit: 176 columns of I
 constexpr int kDnT = 2 * kNc;           // tiles per down unit: 352 columns of H
@@ -160,34 +164,6 @@ __device__ __forceinline__ int lds_read4_now(const void* p) {
     return r;
 }
 
-// LDS counters of the ring (written with single-lane LDS atomics, read with
-// asm reads so that a producer's read never waits for its loads in flight).
-struct Sync {
-    int plan_cnt;          // plans published: slots 0 .. plan_cnt-1
-    int full[4];           // per ring position: producer waves done with the slot's data (2 per slot)
-    int empty[4];          // per ring position: consumer waves done with the slot (kNc per slot)
-    int sig[8];            // finished gate/up units, per plan entry of the unit's last slot
-};
-constexpr int kSyncWords = static_cast<int>(sizeof(Sync) / 4);
-__device__ __forceinline__ int lds_ld(const int* p) { return ruf(lds_read4_now(p)); }
-__device__ __forceinline__ void lds_inc(int* p) {
-    if ((threadIdx.x & (kWave - 1)) == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(lds_off(p)), "v"(1) : "memory");
-}
-__device__ __forceinline__ void lds_put(int* p, int v) {
-    if ((threadIdx.x & (kWave - 1)) == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_off(p)), "v"(v) : "memory");
-}
-constexpr int kMaxSpin = 1 << 23;  // polls of an LDS counter before a wait gives up (about a second)
-// Wait until *p >= target (LDS); on running out of the bound, set the error word and go on.
-__device__ __forceinline__ void lds_wait_ge(const int* p, int target, int32_t* errw) {
-    for (int it = 0; lds_ld(p) < target; ++it) {
-        if (it >= kMaxSpin) {
-            if ((threadIdx.x & (kWave - 1)) == 0) __hip_atomic_store(errw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
 // Compute units of the current device (cached per device).
 int ffn_cus() {
     constexpr int kMaxDev = 64;
@@ -256,18 +232,25 @@ __device__ __forceinline__ int pack_src(const FfnArgs& A, const Plan& p, const u
     return p.nt * kDnTailB;
 }
 
-__device__ __forceinline__ int issue_pack(const FfnArgs& A, const Plan& p, char* slot) {
+// Half h of a slot's pack bytes: the 1 KB instructions d0 .. d1-1 of the
+// slot's nd (wave 0 the first ceil(nd/2), wave 1 the rest with the partial
+// last one). Issues them when ISSUE; returns how many there are.
+template <bool ISSUE>
+__device__ __forceinline__ int issue_pack_half(const FfnArgs& A, const Plan& p, char* slot, int h) {
     if (p.kind < kGu || p.kind > kDnTail) return 0;
     const int lane = threadIdx.x & (kWave - 1);
     const uint8_t* src;
     const int len = pack_src(A, p, src);
     const int nfull = len >> 10, rem = (len & 1023) >> 4;
-    for (int d = 0; d < nfull; ++d) dma16(src + d * 1024 + lane * 16, slot + d * 1024);
-    if (rem) {
-        if (lane < rem) dma16(src + nfull * 1024 + lane * 16, slot + nfull * 1024);
-        return nfull + 1;
+    const int nd = nfull + (rem ? 1 : 0), half = (nd + 1) >> 1;
+    const int d0 = h ? half : 0, d1 = h ? nd : half;
+    if constexpr (ISSUE) {
+        for (int d = d0; d < d1; ++d) {
+            if (d < nfull) dma16(src + d * 1024 + lane * 16, slot + d * 1024);
+            else if (lane < rem) dma16(src + d * 1024 + lane * 16, slot + d * 1024);
+        }
     }
-    return nfull;
+    return d1 - d0;
 }
 
 // Activation blocks of one slot: block (t, i) = 16 rows x 64 bytes (MFMA step
@@ -311,10 +294,12 @@ __device__ __forceinline__ int issue_act(const FfnArgs& A, const Plan& p, char* 
     return nstep * mt;
 }
 
-// The two producer waves share this loop; only the issue differs.
-template <int MTX, int R, bool WEIGHTS>
+// The three producer waves share this loop (ROLE 0, 1: the two halves of each
+// slot's weights; 2: the activations); only the issue differs.
+template <int MTX, int R, int ROLE>
 __device__ void ffn_produce(const FfnArgs& A, char* lds, const Plan* plans, const int* toks) {
     using L = Lay<MTX>;
+    constexpr bool WEIGHTS = ROLE < 2;
     const int lane = threadIdx.x & (kWave - 1);
     const int rr = lane >> 2;
     int tok[MTX];
@@ -332,7 +317,7 @@ __device__ void ffn_produce(const FfnArgs& A, char* lds, const Plan* plans, cons
         }
         char* slot = lds + (k % R) * L::kSlot;
         if constexpr (WEIGHTS) {
-            return issue_pack(A, p, slot);
+            return issue_pack_half<true>(A, p, slot, ROLE);
         } else {
             if (p.kind == kGu && (p.flags & kFirst)) {
                 const int* tk = toks + (k & (kPlanN - 1)) * kWave;
@@ -355,13 +340,14 @@ __device__ void ffn_produce(const FfnArgs& A, char* lds, const Plan* plans, cons
         e0 = min(R - 1, A.G);
         for (int g = 0; g < e0; ++g) {
             p.g = g;
-            win[g] = issue_pack(A, p, lds + g * L::kSlot);
+            win[g] = issue_pack_half<true>(A, p, lds + g * L::kSlot, ROLE);
         }
     }
     __builtin_amdgcn_s_barrier();  // B_init: plans 0 .. R-1 are written
     asm volatile("" ::: "memory");
     // Issue first, then wait: at most R-1 slots are in flight, so a wave keeps
-    // fewer than 64 memory instructions outstanding (vmcnt's range).
+    // fewer than 64 memory instructions outstanding (vmcnt's range: 3 slots of
+    // at most 13 weight or 8 activation instructions).
     for (int k = e0; k < R - 1; ++k)
         if (k < k_end) win[k] = issue(k);
     {
@@ -455,7 +441,8 @@ __device__ __forceinline__ void gu_epilogue(const FfnArgs& A, const Plan& p, con
         }
 }
 
-template <int MTX, int MT, bool TAILS>
+// Down slot of a wave that owns NT2 (1 or 2) tiles: 2w and, for 2, 2w+1.
+template <int MTX, int MT, bool TAILS, int NT2>
 __device__ __forceinline__ void dn_slot(const char* __restrict__ sp, int nt, f32x4 (&acc)[2][MTX],
                                         const NibConsts& kn) {
     const int w = wave_id_ffn();
@@ -463,34 +450,30 @@ __device__ __forceinline__ void dn_slot(const char* __restrict__ sp, int nt, f32
     const int col = lane & 15, c = lane >> 4;
     const int fo = frag_pos(col, c) * 16;
     constexpr int NS = TAILS ? 2 : 4;
-    u32x4 wq[2];
-    f16x2 sz[2];
-    bool on[2];
+    u32x4 wq[NT2];
+    f16x2 sz[NT2];
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
+    for (int v = 0; v < NT2; ++v) {
         const int u = 2 * w + v;
-        on[v] = u < nt;
-        const int uu = on[v] ? u : 0;
         if constexpr (TAILS) {
-            const u32x2 t2 = *reinterpret_cast<const u32x2*>(sp + uu * 512 + lane * 8);
+            const u32x2 t2 = *reinterpret_cast<const u32x2*>(sp + u * 512 + lane * 8);
             wq[v] = u32x4{t2[0], t2[1], 0u, 0u};
-            sz[v] = *reinterpret_cast<const f16x2*>(sp + nt * 512 + uu * 64 + col * 4);
+            sz[v] = *reinterpret_cast<const f16x2*>(sp + nt * 512 + u * 64 + col * 4);
         } else {
-            wq[v] = *reinterpret_cast<const u32x4*>(sp + uu * 1024 + lane * 16);
-            sz[v] = *reinterpret_cast<const f16x2*>(sp + nt * 1024 + uu * 128 + col * 8 + (c >> 1) * 4);
+            wq[v] = *reinterpret_cast<const u32x4*>(sp + u * 1024 + lane * 16);
+            sz[v] = *reinterpret_cast<const f16x2*>(sp + nt * 1024 + u * 128 + col * 8 + (c >> 1) * 4);
         }
     }
-    ZeroPair zc[2];
+    ZeroPair zc[NT2];
 #pragma unroll
-    for (int v = 0; v < 2; ++v) zc[v] = zero_pair(sz[v][1]);
+    for (int v = 0; v < NT2; ++v) zc[v] = zero_pair(sz[v][1]);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
         f16x8 a[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) a[t] = *reinterpret_cast<const f16x8*>(sp + kSlotW + (t * 4 + i) * 1024 + fo);
 #pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            if (!on[v]) continue;
+        for (int v = 0; v < NT2; ++v) {
             const f16x8 b = nib8_dequant(wq[v][i], zc[v], f16x2{sz[v][0], sz[v][0]}, kn);
 #pragma unroll
             for (int t = 0; t < MT; ++t) acc[v][t] = mfma16x16x32(b, a[t], acc[v][t]);
@@ -532,10 +515,14 @@ __device__ __forceinline__ void consume_mt(const FfnArgs& A, const Plan& p, cons
         }
     } else {
         if (2 * w < p.nt) {
-            if (p.kind == kDnFull)
-                dn_slot<MTX, MT, false>(sp, p.nt, acc, kn);
-            else
-                dn_slot<MTX, MT, true>(sp, p.nt, acc, kn);
+            const bool two = 2 * w + 1 < p.nt;
+            if (p.kind == kDnFull) {
+                if (two) dn_slot<MTX, MT, false, 2>(sp, p.nt, acc, kn);
+                else dn_slot<MTX, MT, false, 1>(sp, p.nt, acc, kn);
+            } else {
+                if (two) dn_slot<MTX, MT, true, 2>(sp, p.nt, acc, kn);
+                else dn_slot<MTX, MT, true, 1>(sp, p.nt, acc, kn);
+            }
             if (p.flags & kLast) dn_epilogue<MTX, MT>(A, p, acc);
         }
     }
@@ -757,7 +744,7 @@ __device__ void ffn_control(const FfnArgs& A, const Plan* plans_c, int* toks, in
         if (busy) return;
         if (nx_state == kDepWait && dep_ok) nx_state = kReady;
         if (nx_state == kNeedPull) {
-            int v;
+            int v = 0;
             if (lane == 0) v = __hip_atomic_fetch_add(qctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             pull_v = v;  // lane 0's value is read (readfirstlane) when the batch is taken
             nx_state = kPulled;
@@ -894,13 +881,19 @@ __global__ __launch_bounds__(kFfnThreads) void ffn_kernel(FfnArgs A) {
     int* sig = xdn + (A.E + 1);  // kPlanN counters of finished gate/up units
     if (threadIdx.x < kPlanN) sig[threadIdx.x] = 0;
     const int wave = wave_id_ffn();
+    // The producer and control waves issue first on their SIMD: the arbiter
+    // favours older waves, and the consumers (waves 0 .. kNc-1) would
+    // otherwise delay every load issue after a barrier.
+    if (wave >= kNc) __builtin_amdgcn_s_setprio(3);
     if (wave < kNc)
         ffn_consume<ACT, MTX, R>(A, lds, plans, sig);
-    else if (wave == kWaveW)
-        ffn_produce<MTX, R, true>(A, lds, plans, toks);
+    else if (wave == kWaveW0)
+        ffn_produce<MTX, R, 0>(A, lds, plans, toks);
+    else if (wave == kWaveW1)
+        ffn_produce<MTX, R, 1>(A, lds, plans, toks);
     else if (wave == kWaveA)
-        ffn_produce<MTX, R, false>(A, lds, plans, toks);
-    else
+        ffn_produce<MTX, R, 2>(A, lds, plans, toks);
+    else if (wave == kWaveCtl)
         ffn_control<MTX, R>(A, plans, toks, offs, xgu, xdn);
 }
 
@@ -920,7 +913,7 @@ size_t ffn_lds_bytes(int E) {
 __global__ __launch_bounds__(256) void pack_gateup_kernel(const uint8_t* __restrict__ q, const f16* __restrict__ s,
                                                           const f16* __restrict__ z, uint8_t* __restrict__ out,
                                                           int E, int H, int I) {
-    const int G = H / 128, ncb = (I / 16 + kGuT - 1) / kGuT;
+    const int G = H / 128;
     const int64_t per_e = static_cast<int64_t>(I) * H / 16 * 17 / 16;  // 16-byte units per expert
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= per_e * E) return;
@@ -1047,7 +1040,7 @@ bool ffn_set_lds(const void* fn) {
 }
 
 constexpr int kFfnMtx = 2;  // rows per chunk: 32
-constexpr int kFfnR = 3;    // ring slots (two in flight)
+constexpr int kFfnR = 4;    // ring slots (three in flight)
 
 }  // namespace
 

@@ -430,6 +430,9 @@ template <int ACT, int NC, int NP, int R, int MX>
 __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A) {
     using S = GuShape<NC, NP, R, MX>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
+    // Producer waves issue first on their SIMD after each barrier (the arbiter
+    // otherwise favours the older consumer waves).
+    if (wave_id() >= NC) __builtin_amdgcn_s_setprio(3);
     const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
     const int unit = tile / nb_per_e;  // expert, or row block when A.rb > 0
