@@ -129,6 +129,8 @@ def test_fast_sampler_bitwise_tier_is_stock():
     criterion; accept_canvas and the criterion give the stock results bit for bit."""
     fs = load_mod("fast_sampler")
     G, smp = _sampler(1.5)
+    stock_accept = G.EntropyBoundSampler.accept_canvas
+    stock_call = G.StableAndConfidentStoppingCriteria.__call__
     g = torch.Generator().manual_seed(12)
     logits = 2 * torch.randn(2, 16, 50, generator=g)
     cur = torch.randint(0, 50, (2, 16), generator=g)
@@ -148,9 +150,13 @@ def test_fast_sampler_bitwise_tier_is_stock():
         logits.add_(0.0)  # a new version of the tensor: the cache misses
         G.StableAndConfidentStoppingCriteria.__call__(crit, logits.argmax(-1), logits)
         assert fs.stats()["misses"] == 1
+        assert fs.installed() is False
     finally:
         fs.uninstall()
-    assert G.EntropyBoundSampler.accept_canvas is not fs._accept_canvas
+    assert fs.installed() is None
+    assert G.EntropyBoundSampler.accept_canvas is stock_accept
+    assert G.StableAndConfidentStoppingCriteria.__call__ is stock_call
+    assert fs.stats() == {"hits": 1, "misses": 1}
 
 
 def test_sampler_abi_rejects_bad_arguments_without_launching():
