@@ -557,7 +557,7 @@ __device__ void ffn_consume(const FfnArgs& A, const char* lds, const Plan* plans
     asm volatile("" ::: "memory");
     for (int n = 0;; ++n) {
         const Plan p = read_plan(plans, n);
-        if (pend_e >= 0 && ++pend_age >= 2) signal();
+        if (pend_e >= 0 && ++pend_age >= 4) signal();  // four slots later the stores are acknowledged
         if (p.kind == kEnd) break;
         if (p.kind != kNone) {
             if (p.flags & kFirst) {
