@@ -205,6 +205,17 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
                  const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,
                  void* stream);
 
+/* The MOE_NS down pack back to the reference layout (load time, out of
+ * place): ns_q uint8 [E, I/2, H], the layout the reference's preshuffle_T_dn
+ * writes for its _down_nsT_kernel (kernels/fused_moe_w4_v2.py:187-206; in
+ * each 64-K chunk kb, byte row kb*32 + j of column n holds q[kb*64 + j] in
+ * the low and q[kb*64 + 32 + j] in the high nibble) -> dn_q uint8 [E, H, I/2]
+ * (KSL_DN_LAYOUT_REF, byte b = q[2b] | q[2b+1] << 4). H % 64 == 0,
+ * I % 64 == 0, both pointers 8-byte aligned. Follow with ksl_moe_repack_down
+ * for the tiled layout. */
+int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q,
+                              void* stream);
+
 /* Load-time repack of the down weights into the layout the down kernel loads
  * (the reference's precedent is the preshuffled down pack,
  * kernels/fused_moe_w4_v2.py:187-206). Out of place, same size as

@@ -923,6 +923,38 @@ __global__ __launch_bounds__(256) void repack_down_kernel(const uint8_t* __restr
     }
 }
 
+// The MOE_NS down pack back to the reference layout (load time). NS
+// (kernels/fused_moe_w4_v2.py:187-197): per expert [I/2, H]; within each
+// 64-K chunk kb, byte row kb*32 + j of column n holds q[kb*64 + j] (low
+// nibble) and q[kb*64 + 32 + j] (high nibble). Reference: [H, I/2], byte b of
+// row n = q[2b] | q[2b+1] << 4. One workgroup per (expert, chunk, 64 columns):
+// the chunk's 32 x 64 NS bytes go through LDS; each thread then writes 8
+// output bytes (k = 16m .. 16m+15 of one column).
+__global__ __launch_bounds__(256) void unshuffle_ns_down_kernel(const uint8_t* __restrict__ ns,
+                                                                uint8_t* __restrict__ out, int H, int I) {
+    __shared__ uint8_t tile[32][64];
+    const int nt = blockIdx.x, kb = blockIdx.y, e = blockIdx.z, t = threadIdx.x;
+    const int ih = I / 2;
+    const uint8_t* src = ns + (static_cast<int64_t>(e) * ih + kb * 32) * H + nt * 64;
+    {
+        const int r = t >> 3, c8 = (t & 7) * 8;
+        *reinterpret_cast<uint64_t*>(&tile[r][c8]) =
+            *reinterpret_cast<const uint64_t*>(src + static_cast<int64_t>(r) * H + c8);
+    }
+    __syncthreads();
+    const int n = t >> 2, m = t & 3;  // column n, output bytes 8m .. 8m+7 of the chunk
+    uint64_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int k0 = 2 * (8 * m + i);           // first K index of output byte 8m+i (within the chunk)
+        const int hi = k0 >= 32, j = k0 & 31;     // NS row j (and j+1), high nibbles for the second half
+        const uint32_t b0 = tile[j][n], b1 = tile[j + 1][n];
+        const uint32_t q0 = hi ? b0 >> 4 : b0 & 15u, q1 = hi ? b1 >> 4 : b1 & 15u;
+        v |= static_cast<uint64_t>(q0 | (q1 << 4)) << (8 * i);
+    }
+    *reinterpret_cast<uint64_t*>(out + (static_cast<int64_t>(e) * H + nt * 64 + n) * ih + kb * 32 + 8 * m) = v;
+}
+
 }  // namespace
 
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
@@ -1038,6 +1070,22 @@ extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint
     if (nrows < 0) return KSL_ERR_SHAPE;
     return ksl::launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3,
                             static_cast<hipStream_t>(stream), dn_layout, nrows);
+}
+
+extern "C" int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q,
+                                         void* stream) {
+    using namespace ksl;
+    if (E <= 0 || H <= 0 || I <= 0 || H % 64 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (E > 65535 || I / 64 > 65535 || H / 64 > (int64_t(1) << 31) - 1) return KSL_ERR_SHAPE;
+    if (!ns_q || !dn_q) return KSL_ERR_ARG;
+    if (ns_q == dn_q) return KSL_ERR_ARG;  // out of place
+    if (reinterpret_cast<uintptr_t>(ns_q) % 8 || reinterpret_cast<uintptr_t>(dn_q) % 8) return KSL_ERR_ALIGN;
+    hipLaunchKernelGGL(unshuffle_ns_down_kernel,
+                       dim3(static_cast<unsigned>(H / 64), static_cast<unsigned>(I / 64), static_cast<unsigned>(E)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), ns_q, dn_q, static_cast<int>(H),
+                       static_cast<int>(I));
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }
 
 extern "C" int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled,

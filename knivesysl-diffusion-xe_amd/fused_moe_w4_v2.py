@@ -18,12 +18,16 @@ the output is bit-identical run to run.
 Differences from the reference, on purpose:
 - SiLU-gated experts are supported next to tanh-GELU (the reference asserts
   tanh-GELU, :291-308, :332).
-- The preshuffled down pack (MOE_NS, :180-245) is not used; `dn_ns` modules
-  are rejected. Its counterpart here is enable_tiled_down: the same bytes
-  regrouped in the order the down kernel loads them (same results, faster
-  weight stream), flagged by `dn_tiled`.
+- The preshuffled down pack (MOE_NS, :180-245) is not run as such: a
+  module flagged `dn_ns` (enable_ns_down, :200-206) has its down weights
+  converted on first sight to the tiled layout, the same nibbles regrouped
+  in the order the down kernel loads them (enable_tiled_down, flagged by
+  `dn_tiled`). Results are those of the plain pack.
 - zero-points must be integers in [0, 15] (what quantize_w4 writes,
-  kernels/w4a16.py:28); checked once per module.
+  kernels/w4a16.py:28). check_zero_points verifies it with one host sync;
+  the load-time helpers (enable_tiled_down, enable_pack, pack_experts'
+  repack_experts and load helpers) call it, so the forward itself never
+  synchronises the host and can be captured from its first call.
 """
 from __future__ import annotations
 
@@ -82,10 +86,12 @@ def _check_act(exp) -> bool:
 
 
 def _check_weights(exp, E, H, I) -> None:
+    """Shapes, dtypes, contiguity and device of the six buffers (host-side
+    only, no sync); a module in the MOE_NS down layout is converted first."""
     if getattr(exp, "_ksl_weights_checked", False):
         return
     if getattr(exp, "dn_ns", False):
-        raise NotImplementedError("the preshuffled down pack (dn_ns) is not supported; keep dn_q as [E, H, I/2]")
+        enable_tiled_down(exp)
     spec = {
         "gu_q": ((E, 2 * I, H // 2), torch.uint8),
         "gu_s": ((E, 2 * I, H // 128), torch.float16),
@@ -104,12 +110,42 @@ def _check_weights(exp, E, H, I) -> None:
             raise ValueError(f"exp.{name} must be contiguous")
         if not t.is_cuda:
             raise ValueError(f"exp.{name} must be on the GPU")
+    exp._ksl_weights_checked = True
+
+
+@torch.no_grad()
+def check_zero_points(exp) -> None:
+    """Raise unless every zero-point of exp (gu_z, dn_z) is an integer in
+    [0, 15], the kernels' contract. One host sync; once per module (flagged)."""
+    if getattr(exp, "_ksl_zeros_checked", False):
+        return
     for name in ("gu_z", "dn_z"):
         z = getattr(exp, name)
-        ok = bool(((z == z.round()) & (z >= 0) & (z <= 15)).all().item())  # one sync, once per module
+        ok = bool(((z == z.round()) & (z >= 0) & (z <= 15)).all().item())
         if not ok:
             raise ValueError(f"exp.{name}: zero-points must be integers in [0, 15]")
-    exp._ksl_weights_checked = True
+    exp._ksl_zeros_checked = True
+
+
+@torch.no_grad()
+def unshuffle_ns_down(ns_q: torch.Tensor) -> torch.Tensor:
+    """The MOE_NS down pack [E, I/2, H] (kernels/fused_moe_w4_v2.py:187-197)
+    -> a new [E, H, I/2] tensor in the reference layout (ksl_moe_unshuffle_ns_down)."""
+    E, Ih, H = ns_q.shape
+    if not ns_q.is_cuda or ns_q.dtype != torch.uint8 or not ns_q.is_contiguous():
+        raise ValueError("the NS down pack must be a contiguous uint8 tensor on the GPU")
+    out = torch.empty(E, H, Ih, dtype=torch.uint8, device=ns_q.device)
+    rc = _lib.load().ksl_moe_unshuffle_ns_down(_lib.ptr(ns_q), E, H, 2 * Ih, _lib.ptr(out), _lib.stream_of(ns_q))
+    _lib.check(rc, "ksl_moe_unshuffle_ns_down")
+    return out
+
+
+def _same_device(dev, **tensors) -> None:
+    """The kernels dereference every pointer on `dev`: a tensor elsewhere
+    (a CPU routing tensor, a module on another GPU) is refused here."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, the activations on {dev}")
 
 
 def dn_layout(exp) -> int:
@@ -132,21 +168,24 @@ def tiled_down(dn_q: torch.Tensor) -> torch.Tensor:
 def enable_tiled_down(exp, cache: dict | None = None):
     """Swap exp.dn_q to the tiled layout in place (idempotent via the dn_tiled
     flag), as the reference's enable_ns_down swaps in its preshuffled pack
-    (kernels/fused_moe_w4_v2.py:200-206). `cache` maps an original buffer to its
+    (kernels/fused_moe_w4_v2.py:200-206); a module already in that NS layout
+    (dn_ns) is converted from it. Checks the zero-points (check_zero_points).
+    `cache` maps an original buffer to its
     repacked tensor, so modules that share one dn_q (the encoder and decoder
     experts of a layer, kernels/load_w4_checkpoint.py:56-59) keep sharing one."""
     if getattr(exp, "dn_tiled", False):
         return exp
-    if getattr(exp, "dn_ns", False):
-        raise NotImplementedError("the preshuffled down pack (dn_ns) cannot be tiled; keep dn_q as [E, H, I/2]")
     key = (exp.dn_q.data_ptr(), str(exp.dn_q.device))
     t = None if cache is None else cache.get(key)
     if t is None:
-        t = tiled_down(exp.dn_q)
+        ref = unshuffle_ns_down(exp.dn_q) if getattr(exp, "dn_ns", False) else exp.dn_q
+        t = tiled_down(ref)
         if cache is not None:
             cache[key] = t
     exp.dn_q = t
+    exp.dn_ns = False
     exp.dn_tiled = True
+    check_zero_points(exp)
     return exp
 
 
@@ -158,6 +197,7 @@ def pack_weights(exp) -> tuple[torch.Tensor, torch.Tensor]:
     E, twoI, Hh = exp.gu_q.shape
     H, I = 2 * Hh, twoI // 2
     _check_weights(exp, E, H, I)
+    check_zero_points(exp)
     lib = _lib.load()
     st = _lib.stream_of(exp.gu_q)
     gu = torch.empty(int(lib.ksl_moe_pack_gateup_bytes(E, H, I)), dtype=torch.uint8, device=exp.gu_q.device)
@@ -214,6 +254,7 @@ def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: t
     if topk_ids.shape[0] != T or tuple(topk_w.shape) != (T, tk):
         raise ValueError("topk_ids / topk_w must be [T, topk]")
     dev = hidden.device
+    _same_device(dev, topk_ids=topk_ids, topk_w=topk_w, gu_q=exp.gu_q)
     if hidden.stride(1) != 1 or hidden.stride(0) % 8 != 0 or hidden.data_ptr() % 16 != 0:
         hidden = hidden.contiguous()
     ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)

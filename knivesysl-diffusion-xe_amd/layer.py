@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fused_moe_w4_v2 import _check_act, _check_weights, dn_layout, fused_moe_w4_v2, moe_workspace, pack_ptrs
+from .fused_moe_w4_v2 import _check_act, _check_weights, _same_device, dn_layout, fused_moe_w4_v2, moe_workspace, pack_ptrs
 from .fused_rmsnorm import fused_rmsnorm
 
 STAGES = ("route_norm", "gateup", "down", "combine")
@@ -48,6 +48,9 @@ def moe_layer(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float, exp, top
     E, twoI, _ = exp.gu_q.shape
     I = twoI // 2
     x = _prepare(exp, x, E, H, I)
+    if topk_ids.shape[0] != T or tuple(topk_w.shape) != tuple(topk_ids.shape):
+        raise ValueError("topk_ids / topk_w must be [T, topk]")
+    _same_device(x.device, topk_ids=topk_ids, topk_w=topk_w, norm_w=norm_w, gu_q=exp.gu_q)
     ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)
     ids = ids.contiguous()
     w = topk_w.contiguous()
@@ -120,6 +123,9 @@ class LayerRunner:
             raise TypeError(f"LayerRunner was built for {self.act_dtype} activations, got {x.dtype}")
         if tuple(topk_ids.shape) != (T, tk) or tuple(topk_w.shape) != (T, tk):
             raise ValueError(f"topk_ids / topk_w must be [{T}, {tk}]")
+        if x.device != self.device:
+            raise ValueError(f"x is on {x.device}, the runner's buffers on {self.device}")
+        _same_device(x.device, topk_ids=topk_ids, topk_w=topk_w, norm_w=norm_w, gu_q=exp.gu_q)
         ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)
         ids = ids.contiguous()
         w = topk_w.contiguous()

@@ -142,6 +142,17 @@ def tile_down(dn_q: np.ndarray) -> np.ndarray:
     return np.concatenate([main, tail], axis=-1).reshape(E, H, Ih)
 
 
+def preshuffle_ns_down(dn_q: np.ndarray, bk: int = 64) -> np.ndarray:
+    """The reference's MOE_NS down pack (kernels/fused_moe_w4_v2.py:187-197,
+    preshuffle_T_dn): unpack [E, N, K/2] to codes, and within each bk-chunk
+    put q[k0 + j] in the low and q[k0 + bk/2 + j] in the high nibble of byte
+    j; the result is stored transposed, [E, K/2, N]."""
+    E, N, Kh = dn_q.shape
+    codes = unpack_nibbles(dn_q).reshape(E, N, (2 * Kh) // bk, bk)
+    ns = (codes[..., :bk // 2] | (codes[..., bk // 2:] << 4)).astype(np.uint8).reshape(E, N, Kh)
+    return np.ascontiguousarray(ns.transpose(0, 2, 1))
+
+
 def untile_down(tiled: np.ndarray, I: int) -> np.ndarray:
     """Inverse of tile_down: byte b of tile row r is found at its lane unit."""
     E, H, Ih = tiled.shape

@@ -485,3 +485,27 @@ def test_tile_down_known_answer_and_inverse():
     for I2 in (704, 256):
         qq = np.random.default_rng(I2).integers(0, 256, size=(2, 48, I2 // 2)).astype(np.uint8)
         assert np.array_equal(mo.untile_down(mo.tile_down(qq), I2), qq)
+
+
+# ------------------------------------------------------------------ MOE_NS down pack
+def test_preshuffle_ns_down_brute_force():
+    """The NS pack against the reference's stated byte rule
+    (kernels/fused_moe_w4_v2.py:183-184: within each 64-K chunk, byte j =
+    q[k0+j] | q[k0+32+j] << 4, stored transposed [E, K/2, N]), element by
+    element from the unpacked codes; and a hand-checked position."""
+    rng = np.random.default_rng(5)
+    E, N, K = 2, 8, 192
+    codes = rng.integers(0, 16, size=(E, N, K)).astype(np.uint8)
+    packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)  # w4a16.py:31
+    ns = mo.preshuffle_ns_down(packed)
+    assert ns.shape == (E, K // 2, N)
+    for e in range(E):
+        for n in range(N):
+            for kb in range(K // 64):
+                for j in range(32):
+                    want = codes[e, n, kb * 64 + j] | (codes[e, n, kb * 64 + 32 + j] << 4)
+                    assert ns[e, kb * 32 + j, n] == want
+    # codes 0..63 of one row: NS byte (kb=0, j=1) holds q[1] = 1 low, q[33] = 33 & 15 = 1 high
+    one = (np.arange(64) & 15).astype(np.uint8).reshape(1, 1, 64)
+    pk = (one[..., 0::2] | (one[..., 1::2] << 4)).astype(np.uint8)
+    assert mo.preshuffle_ns_down(pk)[0, 1, 0] == (1 | (1 << 4))
