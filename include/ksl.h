@@ -205,6 +205,19 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
                  const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,
                  void* stream);
 
+/* Asymmetric group-wise 4-bit quantisation (load time): quantize_w4
+ * (kernels/w4a16.py:19-32) as pack_experts_module runs it on every expert
+ * (kernels/pack_experts.py:34-41, 87-106). w: [rows, K] of w_dtype (bf16,
+ * fp16 or fp32; an [E, N, K] expert stack is rows = E*N), contiguous,
+ * pairs of elements aligned; per row and group of group_size columns (32,
+ * 64 or 128; K % group_size == 0), in fp32: scale = max(max - min, 1e-8) / 15,
+ * zero = clamp(round(-min / scale), 0, 15), q = clamp(round(w / scale + zero),
+ * 0, 15) with round-half-to-even; qpacked uint8 [rows, K/2] (byte j =
+ * q[2j] | q[2j+1] << 4), scale / zero fp16 [rows, K/group_size]. The same
+ * bytes, scales and zero-points as the reference. */
+int ksl_quantize_w4(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t group_size, uint8_t* qpacked,
+                    void* scale, void* zero, void* stream);
+
 /* The MOE_NS down pack back to the reference layout (load time, out of
  * place): ns_q uint8 [E, I/2, H], the layout the reference's preshuffle_T_dn
  * writes for its _down_nsT_kernel (kernels/fused_moe_w4_v2.py:187-206; in
