@@ -348,6 +348,20 @@ def combine_fma(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.nda
     return acc
 
 
+def combine_muladd(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.ndarray:
+    """The same chain as combine_fma with `acc += w * x` NOT contracted: the
+    product rounded to fp32, then the sum rounded to fp32. Not the reference's
+    form; it measures how many outputs the FMA assumption of combine_fma
+    decides."""
+    T, tk = topk_w.shape
+    acc = np.zeros((T, out3.shape[1]), dtype=np.float32)
+    w32 = topk_w.astype(np.float32)
+    for k in range(tk):
+        rows = out3[inv.reshape(T, tk)[:, k]].astype(np.float32)
+        acc = (acc + (w32[:, k:k + 1] * rows).astype(np.float32)).astype(np.float32)
+    return acc
+
+
 def moe_forward(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
                 topk_ids: np.ndarray, topk_w: np.ndarray, act: int,
                 block_m: int = 32, return_parts: bool = False):

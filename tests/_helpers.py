@@ -38,9 +38,35 @@ def norm_err(out: np.ndarray, ref: np.ndarray):
     return float(d.max() / (np.abs(ref).max() + 1e-9)), float(d.mean() / (np.abs(ref).mean() + 1e-9))
 
 
-# tolerances for the bf16/fp16 MoE outputs (normalised, reference convention)
-MOE_MAX_TOL = 2e-2
-MOE_MEAN_TOL = 1e-2
+# Per-check bars (normalised max, normalised mean) of the MoE outputs against
+# the oracle, each about twice the largest error observed for that check on
+# the MI355X (the observed values are printed in pytest's terminal summary).
+BARS = {                             # observed on the MI355X (max, mean):
+    "gateup": (2.0e-3, 7.0e-4),         # 9.3e-4, 3.3e-4 (out2, all stage cases)
+    "down": (1.1e-3, 5.0e-7),           # 5.1e-4, 2.0e-7 (out3 from the GPU's own out2)
+    "forward": (1.3e-2, 1.0e-3),        # 6.3e-3, 4.9e-4 (bf16 output, drop-in)
+    "dropped_fp16": (9.0e-4, 9.0e-4),   # 4.4e-4, 4.2e-4
+    "layer_256": (1.3e-2, 1.0e-3),      # 6.3e-3, 4.7e-4
+    "prefill_8192": (3.5e-3, 2.0e-5),   # 1.7e-3, 9.6e-6 (192 sampled tokens)
+    "layer_fixture": (4.2e-3, 3.2e-3),  # 2.1e-3, 1.6e-3
+    "ffn_dropin": (6.0e-3, 3.2e-3),     # 2.8e-3, 1.5e-3
+}
+
+# (check, test id, normalised max, normalised mean) of every check_norm_err call
+OBSERVED: list = []
+
+
+def check_norm_err(check: str, out, ref, label: str = ""):
+    """Assert norm_err(out, ref) within BARS[check]; the observed values are
+    recorded for the terminal summary."""
+    import os
+    mx, mean = norm_err(out, ref)
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    OBSERVED.append((check, test, mx, mean))
+    bmax, bmean = BARS[check]
+    print(f"{check} {label}: norm max {mx:.2e} (bar {bmax:.1e}) mean {mean:.2e} (bar {bmean:.1e})", flush=True)
+    assert mx <= bmax and mean <= bmean, f"{check} {label}: norm max {mx:.2e} / mean {mean:.2e} over the bar"
+    return mx, mean
 
 
 def act_unperm(a: np.ndarray, gs: int) -> np.ndarray:

@@ -509,3 +509,29 @@ def test_preshuffle_ns_down_brute_force():
     one = (np.arange(64) & 15).astype(np.uint8).reshape(1, 1, 64)
     pk = (one[..., 0::2] | (one[..., 1::2] << 4)).astype(np.uint8)
     assert mo.preshuffle_ns_down(pk)[0, 1, 0] == (1 | (1 << 4))
+
+
+def test_combine_fma_assumption_at_layer_256():
+    """The combine oracle assumes the reference's `acc += w * x` is one FMA per
+    slot (Triton contracts it). On a layer_256-shaped combine (256 tokens,
+    top-8, H = 2816, softmax top-8 weights) count the outputs that assumption
+    decides: about half of the fp32 sums differ from multiply-then-add, and a
+    few in 10^5 of the bf16 outputs (28 of 720,896 for this seed), so the
+    bit-exact combine claim rests on it for those."""
+    g = np.random.default_rng(17)
+    T, tk, H = 256, 8, 2816
+    out3 = (0.1 * g.standard_normal((T * tk, H))).astype(np.float16)
+    inv = g.permutation(T * tk)
+    logits = g.standard_normal((T, 128))
+    top = np.argsort(-logits, axis=1)[:, :tk]
+    p = np.exp(np.take_along_axis(logits, top, 1))
+    w = (p / p.sum(1, keepdims=True)).astype(np.float32)
+    y_fma = mo.combine_fma(out3, inv, w)
+    y_ma = mo.combine_muladd(out3, inv, w)
+    frac32 = float((y_fma != y_ma).mean())
+    n_bf16 = int((mo.f32_to_bf16(y_fma) != mo.f32_to_bf16(y_ma)).sum())
+    n_f16 = int((y_fma.astype(np.float16) != y_ma.astype(np.float16)).sum())
+    print(f"FMA vs mul-add: fp32 {frac32:.3f} of outputs differ; bf16 {n_bf16} of {T * H}; fp16 {n_f16}")
+    assert 0.3 < frac32 < 0.7
+    assert 0 < n_bf16 < T * H // 1000 and n_bf16 < n_f16
+    assert np.abs(y_fma - y_ma).max() <= 2 * np.spacing(np.abs(y_fma).max())

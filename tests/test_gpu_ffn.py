@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as mo
-from tests._helpers import MOE_MAX_TOL, MOE_MEAN_TOL, bf16_bits, norm_err
+from tests._helpers import bf16_bits, check_norm_err
 from tests.conftest import load_mod, load_pkg
 
 pytestmark = pytest.mark.gpu
@@ -167,9 +167,7 @@ def test_drop_in_forward_same_with_and_without_pack(gpu):
     dn_q = mo.untile_down(exp.dn_q.cpu().numpy(), I)
     ref, _, _ = mo.moe_forward_per_expert(hidden.float().cpu().numpy(), *qs, dn_q, exp.dn_s.cpu().numpy(),
                                           exp.dn_z.cpu().numpy(), ids.numpy(), w.numpy(), mo.ACT_SILU)
-    mx, mean = norm_err(y1.float().cpu().numpy(), ref)
-    print(f"fused_moe_w4_v2 with the pack: norm max {mx:.2e} mean {mean:.2e}", flush=True)
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("ffn_dropin", y1.float().cpu().numpy(), ref, "fused_moe_w4_v2 with the pack")
 
 
 def test_layer_runner_ffn_stages_match_the_fused_call(gpu):

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests._helpers import MOE_MAX_TOL, MOE_MEAN_TOL, bits_to_bf16_tensor, bf16_bits, norm_err, ulp_diff16
+from tests._helpers import bits_to_bf16_tensor, bf16_bits, check_norm_err, ulp_diff16
 from tests.conftest import load_mod
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -54,6 +54,4 @@ def test_layer_vs_fixture(gpu, act):
     w = torch.from_numpy(f["topk_w"]).to(gpu)
     y = layer.moe_layer(x, nw, float(f["eps"]), exp, ids, w)
     got = y.float().cpu().numpy()
-    mx, mean = norm_err(got, f[f"y_{act}"])
-    print(f"layer fixture {act}: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("layer_fixture", got, f[f"y_{act}"], act)

@@ -18,7 +18,7 @@ import torch
 
 from oracle import moe_oracle as mo
 from oracle import oracle_c
-from tests._helpers import MOE_MAX_TOL, MOE_MEAN_TOL, act_unperm, bf16_bits, f16_bits, norm_err, out2_unperm
+from tests._helpers import act_unperm, bf16_bits, check_norm_err, f16_bits, out2_unperm
 from tests.conftest import load_mod, load_pkg
 
 pytestmark = pytest.mark.gpu
@@ -280,6 +280,7 @@ STAGE_CASES = [
     (200, 2, 4, 256, 832, 38),    # 6.5 128-groups: a 64-K tail, 64-column gate/up blocks
     (192, 2, 3, 256, 1024, 39),   # the largest I (16 64-groups)
     (1100, 8, 12, 256, 768, 40),  # 8800 rows: row blocks with I >= 768
+    (8, 8, 128, 2816, 704, 41),   # 64 rows over 128 experts: most experts empty, one producer without early issue
 ]
 
 
@@ -296,9 +297,8 @@ def test_gateup_and_down_stages(gpu, act, T, tk, E, H, I, seed):
                                                 ids.numpy(), np.ones((T, tk), np.float32), ACTS[act])
     inv_np = _np(inv).astype(np.int64)
     got_out2 = out2_unperm(_np(out2), I)[inv_np]        # back to expanded-row order
-    mx, mean = norm_err(got_out2.astype(np.float32), ref_out2.astype(np.float32))
-    print(f"gate/up {act} T={T} E={E} H={H} I={I}: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("gateup", got_out2.astype(np.float32), ref_out2.astype(np.float32),
+                   f"{act} T={T} E={E} H={H} I={I}")
     # down, isolated: the oracle consumes the GPU's own out2
     flat = ids.numpy().reshape(-1)
     ref_out3 = np.zeros((T * tk, H), dtype=np.float16)
@@ -307,9 +307,7 @@ def test_gateup_and_down_stages(gpu, act, T, tk, E, H, I, seed):
         if r.size:
             ref_out3[r] = mo.down(got_out2[r], mo.dequant_w4(dn_q[e], dn_s[e], dn_z[e], mo.DN_GS))
     got_out3 = _np(out3)[inv_np]
-    mx, mean = norm_err(got_out3.astype(np.float32), ref_out3.astype(np.float32))
-    print(f"down {act} T={T} E={E}: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("down", got_out3.astype(np.float32), ref_out3.astype(np.float32), f"{act} T={T} E={E}")
 
 
 @pytest.mark.parametrize("wdt", [torch.float32, torch.float16])
@@ -367,10 +365,8 @@ def test_forward_vs_oracle(gpu, T, tk, E, H, I, seed, act):
     assert y.dtype == torch.bfloat16 and y.shape == (T, H)
     got = y.float().cpu().numpy()
     ref_b = mo.bf16_to_f32(mo.f32_to_bf16(ref))
-    mx, mean = norm_err(got, ref_b)
-    print(f"forward {act} T={T} E={E} H={H} I={I}: norm max {mx:.2e} mean {mean:.2e} "
-          f"raw max {np.abs(got - ref_b).max():.3e} (|ref| max {np.abs(ref_b).max():.2f})")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("forward", got, ref_b, f"{act} T={T} E={E} H={H} I={I} raw max "
+                   f"{np.abs(got - ref_b).max():.3e} (|ref| max {np.abs(ref_b).max():.2f})")
     # determinism: bit-identical rerun
     y2 = v2.fused_moe_w4_v2(hidden.to(gpu), expg, ids.to(gpu), w.to(gpu))
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
@@ -394,9 +390,7 @@ def test_forward_dropped_rows_and_fp16(gpu):
     gu_q, gu_s, gu_z, dn_q, dn_s, dn_z = _experts_np(exp)
     ref, _, _ = mo.moe_forward_per_expert(hidden.float().numpy(), gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
                                           ids.numpy(), w.numpy(), mo.ACT_GELU_TANH)
-    mx, mean = norm_err(y.float().cpu().numpy(), ref.astype(np.float16).astype(np.float32))
-    print(f"dropped/fp16: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("dropped_fp16", y.float().cpu().numpy(), ref.astype(np.float16).astype(np.float32))
 
 
 def test_layer_256_canvas(gpu):
@@ -418,9 +412,7 @@ def test_layer_256_canvas(gpu):
     # norm parity (<= 1 ulp) is covered in test_gpu_rmsnorm; feed the GPU norm output to the oracle
     ref, _ = _oracle_forward(("layer", 3), xn, exp, ids, w, mo.ACT_SILU)
     ref_b = mo.bf16_to_f32(mo.f32_to_bf16(ref))
-    mx, mean = norm_err(y.float().cpu().numpy(), ref_b)
-    print(f"layer_256: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("layer_256", y.float().cpu().numpy(), ref_b)
     y2 = layer.moe_layer(x.to(gpu), nw.to(gpu), 1e-6, expg, ids.to(gpu), w.to(gpu))
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
@@ -440,9 +432,7 @@ def test_prefill_8192_zipf_sampled_tokens(gpu):
     sample = torch.from_numpy(np.random.default_rng(0).choice(T, 192, replace=False))
     ref, _ = _oracle_forward(("prefill", 4), hidden[sample], exp, ids[sample], w[sample], mo.ACT_SILU)
     ref_b = mo.bf16_to_f32(mo.f32_to_bf16(ref))
-    mx, mean = norm_err(y[sample].float().numpy(), ref_b)
-    print(f"prefill sample: norm max {mx:.2e} mean {mean:.2e}")
-    assert mx <= MOE_MAX_TOL and mean <= MOE_MEAN_TOL
+    check_norm_err("prefill_8192", y[sample].float().numpy(), ref_b, "192 sampled tokens")
 
 
 
@@ -490,9 +480,13 @@ def test_tiled_down_forward_is_bit_identical(gpu, T, tk, E, H, I, seed):
 @pytest.mark.parametrize("T,tk,E,H,I,zipf,seed", [(1200, 8, 16, 256, 128, None, 91), (2048, 8, 128, 512, 256, 1.1, 92)])
 def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
     """Above 8192 routed rows gate/up and down give each workgroup a block of
-    at most 128 rows of one expert; the rows' values do not depend on the
-    split: gate/up and down outputs equal the one-workgroup-per-expert mode
-    (selected here by a small row count) bit for bit."""
+    at most 128 rows of one expert. At the 128- and 64-column gate/up shapes
+    run here (I = 128, 256) both modes use the same decode, so the gate/up and
+    down outputs equal the one-workgroup-per-expert mode (selected by a small
+    row count) bit for bit. At I = 704 the row-block gate/up multiplies the
+    fp16-dequantised weights instead (the reference's rounding), so its bits
+    differ from the small-routing form; that case (8800 rows) is compared with
+    the oracle on every row by test_gateup_and_down_stages."""
     lib = load_pkg()._lib
     wl = load_mod("workloads")
     L = lib.load()
