@@ -205,6 +205,12 @@ int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, 
                  const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,
                  void* stream);
 
+/* Dynamic LDS bytes a ksl_moe_down launch requests for an (E, H, I) layer on
+ * a device with cus compute units (host-only arithmetic, no device call; 0
+ * for a shape outside the contract). Each workgroup also holds 16 bytes of
+ * static LDS; the two together stay within gfx950's 160 KB per workgroup. */
+size_t ksl_moe_down_lds_bytes(int64_t E, int64_t H, int64_t I, int64_t cus);
+
 /* Asymmetric group-wise 4-bit quantisation (load time): quantize_w4
  * (kernels/w4a16.py:19-32) as pack_experts_module runs it on every expert
  * (kernels/pack_experts.py:34-41, 87-106). w: [rows, K] of w_dtype (bf16,

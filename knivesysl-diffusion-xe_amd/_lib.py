@@ -44,6 +44,7 @@ SIGNATURES = {
     "ksl_moe_gateup_act": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P], _I),
     "ksl_moe_down": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I, _P], _I),
     "ksl_quantize_w4": ([_P, _I, _I64, _I64, _I64, _P, _P, _P, _P], _I),
+    "ksl_moe_down_lds_bytes": ([_I64, _I64, _I64, _I64], _SZ),
     "ksl_moe_unshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),

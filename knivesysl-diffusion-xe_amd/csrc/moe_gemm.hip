@@ -32,7 +32,9 @@
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
 // rows (one or two 16-row M tiles); above 8192 routed rows one workgroup per
-// block of at most 64 rows of an expert. Workgroups are remapped so that all
+// block of rows of an expert: 128-row blocks for gate/up (I % 176 == 0:
+// 128-row chunks, eight M tiles per decoded fragment), 64-row blocks for
+// down and for the other gate/up widths. Workgroups are remapped so that all
 // column blocks of an expert run on the same XCD (shared L2 for its
 // activations).
 #include <algorithm>
@@ -47,7 +49,6 @@ namespace {
 constexpr int kXcds = 8;
 constexpr int kRowBlock = 64;        // rows per workgroup block of a large routing
 constexpr int kRowBlockFrom = 8192;  // routed rows above which experts split into row blocks
-constexpr bool kGuRows128 = true;     // gate/up over row blocks: 12 waves, 128-row chunks and blocks
 
 // Index of the calling wave in its workgroup, in a scalar register (branches
 // on it are uniform).
@@ -128,6 +129,10 @@ __device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offse
 constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
 
 constexpr size_t kLdsBytes = 160 * 1024;         // LDS per workgroup on gfx950
+// Static LDS of these kernels (find_row_block's int[3]), rounded up; the
+// dynamic LDS of a launch is sized against what is left.
+constexpr size_t kLdsStatic = 64;
+constexpr size_t kLdsDynMax = kLdsBytes - kLdsStatic;
 constexpr int kGuMaxG = 32;                      // H <= 4096
 
 struct GuArgs {
@@ -151,7 +156,7 @@ struct GuShape {
     static constexpr int kSlotW = 2 * NC * kBlk;               // weight bytes per slot
     static constexpr int kSlot = kSlotW + 4 * MX * kBlk;       // + activation bytes per slot (MX M tiles)
     static constexpr int kSzPer = (4 * kCols * kGuMaxG * 2 / 16 + NC * kWave - 1) / (NC * kWave);
-    static size_t lds_bytes(int G) { return static_cast<size_t>(R) * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
+    static constexpr size_t lds_bytes(int G) { return static_cast<size_t>(R) * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
 };
 
 // Producer side of one row chunk: 1 + G barriers. Slot of group g: g % R.
@@ -530,7 +535,7 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
 
 // Dynamic LDS beyond 64 KB: raise a kernel's limit (called once per kernel).
 bool set_max_lds(const void* fn) {
-    const bool ok = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes) == hipSuccess;
+    const bool ok = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsDynMax) == hipSuccess;
     (void)hipGetLastError();
     return ok;
 }
@@ -563,7 +568,7 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
     if (units * (A.I / S::kCols) >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const unsigned grid = static_cast<unsigned>(units * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
-    if (lds > kLdsBytes) return KSL_ERR_SHAPE;
+    if (lds > kLdsDynMax) return KSL_ERR_SHAPE;
     static const bool attr_set =
         set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R, MX>)) &&
         set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R, MX>));
@@ -990,21 +995,38 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // One workgroup per expert with 176 columns: 11 consumers and one
     // producer wave (12 waves, 3 per SIMD), ring depth 3
     if (I % 176 == 0) {
-        // row blocks (prefill): chunks of up to 64 rows, four M tiles per
-        // decoded weight fragment, ring depth 3 (the slots hold 16 KB of
-        // activations)
-        if (A.rb > 0 && kGuRows128 && GuShape<11, 1, 2, 8>::lds_bytes(H / 128) <= kLdsBytes) {
+        // row blocks (prefill): 128-row blocks and chunks, eight M tiles per
+        // decoded weight fragment, ring depth 2 (the slots hold 32 KB of
+        // activations); both shapes fit at the largest H (static_asserts)
+        static_assert(GuShape<11, 1, 2, 8>::lds_bytes(kGuMaxG) <= kLdsDynMax, "row-block gate/up LDS");
+        static_assert(GuShape<11, 1, 3>::lds_bytes(kGuMaxG) <= kLdsDynMax, "gate/up LDS");
+        if (A.rb > 0) {
             A.rb = 128;
             return launch_gateup_nc<11, 1, 2, 8>(A, E, nrows_hint, act, st);
         }
-        if (A.rb > 0 && GuShape<11, 5, 3, 4>::lds_bytes(H / 128) <= kLdsBytes)
-            return launch_gateup_nc<11, 5, 3, 4>(A, E, nrows_hint, act, st);
-        if (GuShape<11, 1, 3>::lds_bytes(H / 128) <= kLdsBytes)
-            return launch_gateup_nc<11, 1, 3>(A, E, nrows_hint, act, st);
-        return launch_gateup_nc<11, 5, 3>(A, E, nrows_hint, act, st);
+        return launch_gateup_nc<11, 1, 3>(A, E, nrows_hint, act, st);
     }
     if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, nrows_hint, act, st);
     return launch_gateup_nc<4, 4, 4>(A, E, nrows_hint, act, st);
+}
+
+// Column split of the down launch: each expert's H/16 column tiles go to
+// nsplit workgroups of tpw tiles, enough workgroups to fill the CUs and few
+// enough tiles that their scale / zero rows fit in LDS beside the
+// activations (the static LDS reserved).
+struct DnPlan {
+    int64_t tpw, nsplit;
+    size_t lds;
+};
+DnPlan plan_down(int64_t E, int64_t H, int64_t I, int cus) {
+    const int G = static_cast<int>(I / 64);
+    const int64_t te = H / 16;  // 16-column tiles per expert
+    const int64_t max_tiles = static_cast<int64_t>((kLdsDynMax - dn_lds_bytes(G, 0)) / (static_cast<size_t>(16) * G * 4));
+    int64_t nsplit = std::max<int64_t>((cus + E - 1) / E, (te + max_tiles - 1) / max_tiles);
+    nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, te));
+    const int64_t tpw = (te + nsplit - 1) / nsplit;
+    nsplit = (te + tpw - 1) / tpw;
+    return DnPlan{tpw, nsplit, dn_lds_bytes(G, static_cast<int>(tpw * 16))};
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
@@ -1031,19 +1053,12 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     A.rb = nrows > kRowBlockFrom ? kRowBlock : 0;
     const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
     const int G = static_cast<int>(I / 64);
-    // columns per workgroup: enough workgroups to fill the CUs, few enough
-    // columns that their scale / zero rows fit in LDS beside the activations
-    const int64_t te = H / 16;  // 16-column tiles per expert
-    const int64_t max_tiles = static_cast<int64_t>((kLdsBytes - dn_lds_bytes(G, 0)) / (static_cast<size_t>(16) * G * 4));
-    int64_t nsplit = std::max<int64_t>((device_cus() + E - 1) / E, (te + max_tiles - 1) / max_tiles);
-    nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, te));
-    const int64_t tpw = (te + nsplit - 1) / nsplit;
-    nsplit = (te + tpw - 1) / tpw;
-    A.tpw = static_cast<int>(tpw);
-    A.nsplit = static_cast<int>(nsplit);
-    const int64_t grid = units * nsplit;
+    const DnPlan plan = plan_down(E, H, I, device_cus());
+    A.tpw = static_cast<int>(plan.tpw);
+    A.nsplit = static_cast<int>(plan.nsplit);
+    const int64_t grid = units * plan.nsplit;
     if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
-    const size_t lds = dn_lds_bytes(G, static_cast<int>(tpw * 16));
+    const size_t lds = plan.lds;
     switch (G) {
 #define KSL_DN_CASE(GG) \
     case GG: return launch_down_g<GG / 2, (GG % 2) != 0>(A, static_cast<unsigned>(grid), lds, layout, st);
@@ -1070,6 +1085,11 @@ extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint
     if (nrows < 0) return KSL_ERR_SHAPE;
     return ksl::launch_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3,
                             static_cast<hipStream_t>(stream), dn_layout, nrows);
+}
+
+extern "C" size_t ksl_moe_down_lds_bytes(int64_t E, int64_t H, int64_t I, int64_t cus) {
+    if (E <= 0 || H <= 0 || I <= 0 || cus <= 0 || H % 16 != 0 || I % 64 != 0 || I > 1024) return 0;
+    return ksl::plan_down(E, H, I, static_cast<int>(cus)).lds;
 }
 
 extern "C" int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q,

@@ -141,3 +141,24 @@ def test_block_tail_entry_points_reject_bad_arguments_without_launching():
     assert block(h1=null) == 1
     assert block() == 5                                       # workspace missing
     assert block(T=0) == 0
+
+
+def test_down_lds_sizing_leaves_room_for_static_lds(L):
+    """ksl_moe_down's column split keeps dynamic LDS + the kernel's 16 bytes
+    of static LDS (find_row_block's int[3]) within gfx950's 160 KB, over the
+    corners of the contract (E <= 512, H <= 4096, I <= 1024) and device sizes
+    from 1 to 1024 CUs, including the shapes where the split is limited by
+    LDS rather than by the CU count (E=128, H=4096, I=1024; E=256, H=3072, I=512)."""
+    static = 16
+    worst = 0
+    for E in (1, 8, 128, 256, 512):
+        for H in (128, 256, 2816, 3072, 4096):
+            for I in (64, 128, 512, 704, 768, 1024):
+                for cus in (1, 80, 256, 304, 1024):
+                    lds = L.ksl_moe_down_lds_bytes(E, H, I, cus)
+                    assert lds > 0, (E, H, I, cus)
+                    assert lds + static <= 160 * 1024, (E, H, I, cus, lds)
+                    worst = max(worst, lds)
+    assert worst > 150 * 1024  # the LDS-limited shapes are among the cases
+    assert L.ksl_moe_down_lds_bytes(128, 4096, 1088, 256) == 0  # I above the contract
+    assert L.ksl_moe_down_lds_bytes(128, 4096, 100, 256) == 0   # I % 64 != 0

@@ -275,7 +275,7 @@ STAGE_CASES = [
     (256, 8, 128, 2816, 704, 33),
     (48, 4, 8, 384, 704, 34),    # odd number of 128-groups, 176-column blocks
     (40, 4, 4, 640, 128, 35),    # odd number of 128-groups, 128-column blocks
-    (1100, 8, 12, 256, 704, 36),  # 8800 rows: row blocks, chunks of up to 64 rows (four M tiles)
+    (1100, 8, 12, 256, 704, 36),  # 8800 rows: 128-row gate/up blocks and chunks, 64-row down blocks
     # I >= 768: down takes chunks of two M tiles (32 rows), experts of ~130-200 rows
     (200, 2, 4, 256, 832, 38),    # 6.5 128-groups: a 64-K tail, 64-column gate/up blocks
     (192, 2, 3, 256, 1024, 39),   # the largest I (16 64-groups)
@@ -513,3 +513,33 @@ def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
     torch.cuda.synchronize()
     assert torch.equal(outs2[0].view(torch.int16), outs2[1].view(torch.int16))
     assert torch.equal(outs3[0].view(torch.int16), outs3[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("E,H,I", [(128, 4096, 1024), (256, 3072, 512)])
+def test_down_at_lds_limited_shapes(gpu, E, H, I):
+    """The down launch at the contract's shapes whose column split is limited
+    by LDS (not by the CU count): it launches (dynamic + static LDS fit) and
+    matches the oracle on rows of 8 experts."""
+    lib = load_pkg()._lib
+    L = lib.load()
+    g = torch.Generator().manual_seed(E + H + I)
+    dn_q = torch.randint(0, 256, (E, H, I // 2), generator=g, dtype=torch.uint8)
+    dn_s = (0.005 + 0.015 * torch.rand(E, H, I // 64, generator=g)).to(torch.float16)
+    dn_z = torch.randint(0, 16, (E, H, I // 64), generator=g).to(torch.float16)
+    experts = [3, 17, 40, 41, 77, 100, E - 2, E - 1]
+    counts = np.zeros(E, np.int64)
+    counts[experts] = 1
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    out2 = (0.5 * torch.randn(len(experts), I, generator=g)).to(torch.float16)
+    out3 = torch.full((len(experts), H), float("nan"), dtype=torch.float16, device=gpu)
+    offg = torch.from_numpy(offsets).to(gpu)
+    out2g = out2.to(gpu)
+    dq, ds, dz = dn_q.to(gpu), dn_s.to(gpu), dn_z.to(gpu)
+    print(f"ksl_moe_down E={E} H={H} I={I} lds {L.ksl_moe_down_lds_bytes(E, H, I, 256)}", flush=True)
+    lib.check(L.ksl_moe_down(lib.ptr(out2g), lib.ptr(offg), lib.ptr(dq), lib.ptr(ds), lib.ptr(dz), E, H, I,
+                             len(experts), lib.ptr(out3), lib.DN_LAYOUT_REF, lib.stream_of(out3)), "ksl_moe_down")
+    torch.cuda.synchronize()
+    x = out2_unperm(f16_bits(out2).view(np.float16), I)  # logical order of the stored rows
+    ref = np.stack([mo.down(x[i:i + 1], mo.dequant_w4(dn_q[e].numpy(), dn_s[e].numpy(), dn_z[e].numpy(),
+                                                          mo.DN_GS))[0] for i, e in enumerate(experts)])
+    check_norm_err("down", out3.float().cpu().numpy(), ref.astype(np.float32), f"E={E} H={H} I={I}")
