@@ -10,16 +10,27 @@ Synthetic seeded data. Inputs are resident in HBM before the timed region.
 A "step" is one layer. Consecutive steps rotate over independent weight sets
 (3 x 412 MB by default) so the 256 MB MALL cannot serve weights from cache.
 
-Timed passes (all inside this process, same stream):
-  1. value: K steps of the layer (one C call per step, four launches:
-     routing + RMSNorm + fp16 activations, gate/up, down, combine), bracketed
-     by synchronize; µs per layer = elapsed / K.
-  2. per-kernel: K steps issued stage by stage with HIP events between the
-     four launches; the average duration of each kernel, from which the
-     dominant kernel's achieved bandwidth (roofline) is computed.
-  3. cpu_baseline: the reference CPU path (torch eager, oracle/cpu_baseline.py)
-     on the host cores, bounded to ~20 s.
+Timed passes (all inside this process, on one stream):
+  1. value: K steps of the layer (one C call per step: routing + RMSNorm +
+     fp16 activations, gate/up, down, combine; with --ffn gate/up and down
+     are one launch), bracketed by synchronize; µs per layer = elapsed / K.
+  2. per-kernel: each stage's kernel alone, K launches back to back between
+     two HIP events on the same stream (the routing produced once; gate/up
+     and down rotate over the weight sets), giving its average launch
+     duration; achieved GB/s = the kernel's algorithmic bytes / that
+     duration, and the dominant kernel's is the roofline.
+  3. RMSNorm alone at the rmsnorm_256 and rmsnorm_32k (+ qk-norm) shapes.
+  4. cpu_baseline: the reference CPU path (torch eager, oracle/cpu_baseline.py)
+     on every host core of the process's affinity set, bounded to ~20 s.
 Prints ONE JSON line on stdout; progress goes to stderr.
+
+HBM traffic per launch (roofline.traffic) comes from rocprofv3 counter runs
+of this script, reduced by --summarize-pmc into profiles/traffic_layer256.json:
+  rocprofv3 --pmc FETCH_SIZE --output-format csv -d <F> -- python3 bench.py --copy-calibration ...
+  rocprofv3 --pmc WRITE_SIZE --output-format csv -d <W> -- python3 bench.py --copy-calibration ...
+  python3 bench.py --summarize-pmc <F> <W>
+FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are scaled by what they read for
+the copy of known size that --copy-calibration runs.
 """
 from __future__ import annotations
 
@@ -63,6 +74,83 @@ def gateup_algorithmic_bytes(n_experts_touched: int) -> int:
     return (n_experts_touched * GU_EXPERT_BYTES + T * H * 2 + T * TOPK * I * 2 + T * TOPK * 4 + (E + 1) * 4)
 
 
+def down_algorithmic_bytes(n_experts_touched: int) -> int:
+    """Touched experts' down weights, out2 read once, out3 written, offsets."""
+    return n_experts_touched * DN_EXPERT_BYTES + T * TOPK * I * 2 + T * TOPK * H * 2 + (E + 1) * 4
+
+
+def route_norm_algorithmic_bytes() -> int:
+    """x and the norm weight read, the fp16 activations written; ids read;
+    sorted rows, inverse and offsets written."""
+    return T * H * 2 + H * 2 + T * H * 2 + T * TOPK * 8 + 2 * T * TOPK * 4 + (E + 1) * 4
+
+
+def combine_algorithmic_bytes() -> int:
+    """out3 rows read once, the routing weights and inverse read, y written."""
+    return T * TOPK * H * 2 + T * TOPK * (4 + 4) + T * H * 2
+
+
+def stage_bytes(n_touched: int) -> dict:
+    gu, dn = gateup_algorithmic_bytes(n_touched), down_algorithmic_bytes(n_touched)
+    # the one-launch FFN: both weight sets; out2 is written and read back inside
+    return {"route_norm": route_norm_algorithmic_bytes(), "gateup": gu, "down": dn,
+            "ffn": gu + dn - T * TOPK * I * 2, "combine": combine_algorithmic_bytes()}
+
+
+# rocprofv3 kernel names of the stages (substring match on the demangled name)
+STAGE_KERNELS = {"route_norm": "route", "gateup": "gateup_act_kernel", "down": "down_kernel",
+                 "ffn": "ffn_kernel", "combine": "combine_kernel"}
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+    """Per-kernel HBM bytes per dispatch from two rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE; KiB), each scaled by the factor that makes the
+    --copy-calibration copies (512 MiB read + 512 MiB written each) read
+    their known size; writes profiles/traffic_layer256.json."""
+    import csv
+    import glob
+
+    def per_dispatch(d, counter):
+        """{kernel name: {dispatch id: counter value summed over its rows}}"""
+        vals: dict = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter:
+                    k = vals.setdefault(r["Kernel_Name"], {})
+                    k[r["Dispatch_Id"]] = k.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+        return vals
+
+    fd, wd = per_dispatch(fetch_dir, "FETCH_SIZE"), per_dispatch(write_dir, "WRITE_SIZE")
+    fetch = {k: (sum(v.values()) / len(v), len(v)) for k, v in fd.items()}
+    write = {k: (sum(v.values()) / len(v), len(v)) for k, v in wd.items()}
+    copy_bytes = 512 << 20
+
+    def copy_factor(table):
+        # the largest single copy dispatch is one of the 512 MiB calibration copies
+        vals = [x for k, v in table.items() if "copybuffer" in k.lower() for x in v.values()]
+        return copy_bytes / (max(vals) * 1024.0) if vals and max(vals) > 0 else None
+
+    fr, wr = copy_factor(fd), copy_factor(wd)
+    out = {"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --copy-calibration",
+           "unit": "bytes per dispatch", "fetch_scale": fr, "write_scale": wr, "kernels": {}}
+    for stage, key in STAGE_KERNELS.items():
+        names = [k for k in fetch if key in k]
+        if not names:
+            continue
+        name = max(names, key=lambda k: fetch[k][1])
+        f_kib, n = fetch[name]
+        w_kib = write.get(name, (0.0, 0))[0]
+        rd = f_kib * 1024.0 * (fr or 1.0)
+        wt = w_kib * 1024.0 * (wr or 1.0)
+        out["kernels"][stage] = {"kernel": name, "dispatches": n, "fetch_bytes": round(rd),
+                                 "write_bytes": round(wt), "hbm_bytes_per_launch": round(rd + wt)}
+    path = os.path.join(ROOT, "profiles", "traffic_layer256.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,7 +168,12 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed region, copy a 512 MiB buffer 5 times (a kernel of known "
                          "traffic, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--skip-rmsnorm", action="store_true", help="skip the RMSNorm-alone timings")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="reduce two rocprofv3 --pmc output folders to profiles/traffic_layer256.json and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -154,30 +247,102 @@ def main() -> int:
     log(f"[bench] layer: {layer_us:.2f} us/step (events), wall {wall_ms / args.steps * 1e3:.2f} us/step; "
         f"{layer_gbps:.0f} GB/s = {100 * layer_gbps / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
 
-    # ---- pass 2: per-kernel durations with events between launches ----------
+    # ---- pass 2: each stage's kernel alone, back to back ----------------------
     kernels = {}
+    sbytes = stage_bytes(n_touched)
     if not args.skip_kernel_pass:
         stages = runner.stages(sets[0])
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(args.steps)]
-        for i in range(args.warmup):
-            runner.run(xg, nwg, 1e-6, sets[i % len(sets)], idsg, wg)
+        runner.run(xg, nwg, 1e-6, sets[0], idsg, wg)  # routing, a16, out2, out3 for the launches below
         torch.cuda.synchronize()
-        for i in range(args.steps):
-            runner.run(xg, nwg, 1e-6, sets[i % len(sets)], idsg, wg, events=evs[i])
-        torch.cuda.synchronize()
-        for k, name in enumerate(stages):
-            d = sorted(evs[i][k].elapsed_time(evs[i][k + 1]) * 1e3 for i in range(args.steps))
-            kernels[name] = {"avg_us": sum(d) / len(d), "median_us": d[len(d) // 2]}
+        R = runner
+
+        def launch(name, exp):
+            if name == "route_norm":
+                rc = L.ksl_moe_layer_route(p(idsg), T, TOPK, E, p(R.sorted_rows), p(R.offsets), p(R.inv), p(xg),
+                                           lib.DTYPE_BF16, H, p(nwg), lib.DTYPE_BF16, 1e-6, H, p(R.a16),
+                                           p(R.scratch), R.scratch.numel() * 4, st)
+            elif name == "gateup":
+                rc = L.ksl_moe_gateup_act(p(R.a16), p(R.sorted_rows), p(R.offsets), T, TOPK, p(exp.gu_q),
+                                          p(exp.gu_s), p(exp.gu_z), E, H, I, exp._ksl_act, p(R.out2), st)
+            elif name == "down":
+                rc = L.ksl_moe_down(p(R.out2), p(R.offsets), p(exp.dn_q), p(exp.dn_s), p(exp.dn_z), E, H, I,
+                                    T * TOPK, p(R.out3), v2.dn_layout(exp), st)
+            elif name == "ffn":
+                rc = L.ksl_moe_ffn(p(R.a16), p(R.sorted_rows), p(R.offsets), T, TOPK, p(exp.gu_pack),
+                                   p(exp.dn_pack), E, H, I, exp._ksl_act, p(R.out2), p(R.out3), p(R.ctl), st)
+            else:
+                rc = L.ksl_moe_combine(p(R.out3), p(R.inv), p(wg), lib.DTYPE_F32, T, TOPK, H, p(R.y),
+                                       lib.DTYPE_BF16, H, st)
+            if rc:
+                lib.check(rc, name)
+
+        for name in stages:
+            for i in range(args.warmup):
+                launch(name, sets[i % len(sets)])
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(args.steps):
+                launch(name, sets[i % len(sets)])
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / args.steps
+            gbps = sbytes[name] / (us * 1e-6) / 1e9
+            kernels[name] = {"avg_us": round(us, 3), "algorithmic_bytes": sbytes[name], "GBps": round(gbps, 1),
+                             "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
         tot = sum(v["avg_us"] for v in kernels.values())
-        log("[bench] per-kernel avg us: " + ", ".join(f"{k} {v['avg_us']:.2f}" for k, v in kernels.items())
-            + f" (sum {tot:.2f})")
-        # parity of the staged output with the fused call on the same set
+        log("[bench] per-kernel avg us (alone, back to back): "
+            + ", ".join(f"{k} {v['avg_us']:.2f} ({v['GBps']:.0f} GB/s)" for k, v in kernels.items())
+            + f" (sum {tot:.2f}, layer {layer_us:.2f})")
+        # the staged launches give the fused call's bits
         step(sets[0])
         yf = y.clone()
         ys = runner.run(xg, nwg, 1e-6, sets[0], idsg, wg).clone()
         torch.cuda.synchronize()
         if not torch.equal(yf.view(torch.int16), ys.view(torch.int16)):
             log("[bench] WARNING: staged and fused outputs differ")
+
+    # ---- pass 3: RMSNorm alone (rmsnorm_256, rmsnorm_32k + qk-norm) -----------
+    rmsnorm = None
+    if not args.skip_rmsnorm:
+        def norm_us(xs, wt, n):
+            rows, cols = xs[0].shape
+            ys_ = [torch.empty_like(t) for t in xs]
+
+            def one(i):
+                rc = L.ksl_rmsnorm(p(xs[i % len(xs)]), lib.DTYPE_BF16, p(wt), lib.DTYPE_BF16, p(ys_[i % len(xs)]),
+                                   lib.DTYPE_BF16, rows, cols, cols, cols, 1e-6, st)
+                if rc:
+                    lib.check(rc, "ksl_rmsnorm")
+
+            for i in range(5):
+                one(i)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(n):
+                one(i)
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / n
+            nbytes = 2 * rows * cols * 2 + cols * 2
+            return us, nbytes / (us * 1e-6) / 1e9
+
+        x0, w0, _ = wl.rmsnorm_256(0)
+        u256, g256 = norm_us([x0.to(dev)], w0.to(dev), max(100, args.steps))
+        x1, w1, qk, qkw, _ = wl.rmsnorm_32k(1)
+        x1g = [x1.to(dev), x1.roll(1, 0).to(dev)]  # two inputs in turn: 2 x 184 MB, more than the MALL
+        del x1
+        u32k, g32k = norm_us(x1g, w1.to(dev), 50)
+        del x1g
+        uqk, gqk = norm_us([qk.to(dev)], qkw.to(dev), max(100, args.steps))
+        rmsnorm = {"rmsnorm_256_us": round(u256, 3), "rmsnorm_256_GBps": round(g256, 1),
+                   "rmsnorm_32k_us": round(u32k, 3), "rmsnorm_32k_GBps": round(g32k, 1),
+                   "rmsnorm_32k_frac_of_hbm_peak": round(g32k / HBM_PEAK_GBPS, 4),
+                   "qk_norm_4096x256_us": round(uqk, 3), "qk_norm_GBps": round(gqk, 1)}
+        log(f"[bench] rmsnorm alone: [256, {H}] {u256:.2f} us ({g256:.0f} GB/s); [32768, {H}] {u32k:.2f} us "
+            f"({g32k:.0f} GB/s = {100 * g32k / HBM_PEAK_GBPS:.1f}% of 8 TB/s); qk-norm [4096, 256] {uqk:.2f} us")
+        torch.cuda.empty_cache()
 
     # ---- the router (the step before the layer; not part of `value`) --------
     router_us = None
@@ -409,19 +574,20 @@ def main() -> int:
             f"2.5 PFLOP/s dense f16 MFMA peak; kernels " + ", ".join(f"{k} {v:.1f}" for k, v in pk.items()))
         del xpg, yp, wsp, prunner
 
-    gu_bytes = gateup_algorithmic_bytes(n_touched)
     roofline = None
     if kernels:
-        gu_us = kernels["gateup"]["avg_us"] if "gateup" in kernels else kernels["ffn"]["avg_us"]
-        ach = gu_bytes / (gu_us * 1e-6) / 1e9
-        traffic = None
-        tpath = os.path.join(ROOT, "profiles", "traffic_moe_gateup_layer256.json")
+        dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
+        kv = kernels[dom]
+        traffic = traffic_kernel = None
+        tpath = os.path.join(ROOT, "profiles", "traffic_layer256.json")
         if os.path.exists(tpath):
             with open(tpath) as f:
-                traffic = json.load(f).get("hbm_bytes_per_launch")
-        roofline = {"kernel": "gateup_act_kernel", "bound": "hbm", "achieved": round(ach, 1),
-                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                    "traffic": traffic, "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 3)}
+                t = json.load(f).get("kernels", {}).get(dom)
+            if t:
+                traffic, traffic_kernel = t["hbm_bytes_per_launch"], t["kernel"]
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": kv["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": kv["frac_of_hbm_peak"], "traffic": traffic, "traffic_kernel": traffic_kernel,
+                    "algorithmic_bytes": kv["algorithmic_bytes"], "avg_us": kv["avg_us"]}
 
     if args.copy_calibration:
         nbytes = 512 << 20
@@ -473,7 +639,10 @@ def main() -> int:
             "layer_frac_of_hbm_peak": round(layer_gbps / HBM_PEAK_GBPS, 4),
             "compute": "u4 weights, f16 MFMA operands, f32 accumulate, bf16 in/out",
             "parallelism": "single GPU",
-            "kernels_us": {k: round(v["avg_us"], 3) for k, v in kernels.items()},
+            "kernels": kernels,
+            "rmsnorm_256_us": None if rmsnorm is None else rmsnorm["rmsnorm_256_us"],
+            "rmsnorm_32k_us": None if rmsnorm is None else rmsnorm["rmsnorm_32k_us"],
+            "rmsnorm": rmsnorm,
             "router_us": None if router_us is None else round(router_us, 3),
             "block_tail": tail,
             "sampler": sampler,

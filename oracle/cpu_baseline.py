@@ -23,12 +23,13 @@ import torch
 import torch.nn.functional as F
 
 
-def host_threads(cap: int = 16) -> int:
+def host_threads() -> int:
+    """Every core of this process's affinity set (the host's share for the run)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(n, cap))
+    return max(1, n)
 
 
 def rmsnorm_stock(x: torch.Tensor, w: torch.Tensor | None, eps: float) -> torch.Tensor:
