@@ -100,6 +100,14 @@ template <int DT> __device__ __forceinline__ Raw8<DT> raw_load8(const void* p) {
     for (int i = 0; i < (DT == KSL_DTYPE_F32 ? 2 : 1); ++i) r.q[i] = reinterpret_cast<const u32x4*>(p)[i];
     return r;
 }
+// The same load marked non-temporal (data read once: streamed past the caches).
+template <int DT> __device__ __forceinline__ Raw8<DT> raw_load8_nt(const void* p) {
+    Raw8<DT> r;
+#pragma unroll
+    for (int i = 0; i < (DT == KSL_DTYPE_F32 ? 2 : 1); ++i)
+        r.q[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + i);
+    return r;
+}
 template <int DT> __device__ __forceinline__ void raw_unpack8(const Raw8<DT>& r, float (&v)[8]) {
     if constexpr (DT == KSL_DTYPE_BF16) {
 #pragma unroll
@@ -140,6 +148,26 @@ template <> __device__ __forceinline__ void store8<KSL_DTYPE_F32>(void* p, const
     f32x4* q = reinterpret_cast<f32x4*>(p);
     q[0] = f32x4{v[0], v[1], v[2], v[3]};
     q[1] = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+// store8 marked non-temporal (data written once, not read back soon).
+template <int DT> __device__ __forceinline__ void store8_nt(void* p, const float (&v)[8]) {
+    if constexpr (DT == KSL_DTYPE_BF16) {
+        u32x4 q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            q[i] = static_cast<uint32_t>(f32_to_bf16_bits(v[2 * i])) |
+                   (static_cast<uint32_t>(f32_to_bf16_bits(v[2 * i + 1])) << 16);
+        __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(p));
+    } else if constexpr (DT == KSL_DTYPE_F16) {
+        f16x8 q;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = static_cast<f16>(v[i]);
+        __builtin_nontemporal_store(q, reinterpret_cast<f16x8*>(p));
+    } else {
+        __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(p));
+        __builtin_nontemporal_store(f32x4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4*>(p) + 1);
+    }
 }
 
 // ---- W4 nibble decode -------------------------------------------------------
