@@ -653,13 +653,16 @@ struct DnW {
 template <int G2, bool TAIL, int LAYOUT>
 __device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* tbase, int col, int c, int rb) {
     if constexpr (LAYOUT == kDnTiled) {
+        // non-temporal: each weight byte is read once per launch (about 1 us
+        // faster at the 256-token layer than the cached load; the same hint on
+        // gate/up's direct-to-LDS loads costs 15 us there)
         const uint8_t* p = tbase + (c * 16 + col) * 16;
 #pragma unroll
         for (int g2 = 0; g2 < G2; ++g2)
-            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(w.q[g2]) : "v"(p + g2 * 1024) : "memory");
+            asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(w.q[g2]) : "v"(p + g2 * 1024) : "memory");
         if constexpr (TAIL) {
             const uint8_t* pt = tbase + G2 * 1024 + (c * 16 + col) * 8;
-            asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
+            asm volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(w.t[0]) : "v"(pt) : "memory");
         }
     } else {
         const uint8_t* p = tbase + col * rb + c * 16;
@@ -668,7 +671,7 @@ __device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* tbase
             asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w.q[g2]) : "v"(p), "i"(g2 * 64) : "memory");
         if constexpr (TAIL) {
             const uint8_t* pt = tbase + col * rb + G2 * 64 + c * 8;
-            asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(w.t[0]) : "v"(pt) : "memory");
+            asm volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(w.t[0]) : "v"(pt) : "memory");
         }
     }
 }
