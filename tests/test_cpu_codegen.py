@@ -1,0 +1,158 @@
+"""The down kernel's generated code, checked on the CPU.
+
+ksl_moe_down streams each wave's weight tiles through two register buffers
+loaded by inline asm (the compiler's own waits would drain the prefetch), so
+correctness depends on the register allocator never copying or reusing a
+buffer register while its load is in flight. The device assembly of
+csrc/moe_gemm.hip is built with the library's flags and a few workgroups of
+down_kernel are run through tests/gfx950_emu.py: every global, buffer and LDS
+access must stay in its buffer and no address, stored value or MFMA operand
+may come from a register whose load had not landed. Shapes: the 256-token
+layer (one chunk, up to two M tiles), 1024 tokens (four M tiles, several
+chunks per expert), a Zipf routing above 8192 rows (row blocks found through
+LDS), and small / odd I (a 64-K tail group, the largest I)."""
+from __future__ import annotations
+
+import importlib.util
+import os
+import shutil
+import struct
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+import gfx950_emu as emu  # noqa: E402
+
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(ROOT, "knivesysl-diffusion-xe_amd", "csrc")
+
+
+def _build_flags():
+    spec = importlib.util.spec_from_file_location("ksl_build", os.path.join(ROOT, "knivesysl-diffusion-xe_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.HIPCC, mod.HIP_FLAGS
+
+
+@pytest.fixture(scope="module")
+def down_asm(tmp_path_factory):
+    hipcc, flags = _build_flags()
+    if not (os.path.exists(hipcc) or shutil.which(hipcc)):
+        pytest.skip("hipcc not available")
+    out = str(tmp_path_factory.mktemp("asm") / "moe_gemm.s")
+    res = subprocess.run([hipcc, *flags, "-w", "--cuda-device-only", "-S", os.path.join(CSRC, "moe_gemm.hip"),
+                          "-o", out], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-4000:]
+    return out
+
+
+# The launch plan of csrc/moe_gemm.hip (plan_down, kDnWaves, kDnMaxMt, the
+# row-block threshold) restated for the emulated launches.
+NW, MAX_MT, LDS_DYN_MAX, CUS = 12, 4, 160 * 1024 - 64, 256
+
+
+def _plan(E, H, I):
+    G = I // 64
+    te = H // 16
+    base = MAX_MT * 2 * G * 1024
+    max_tiles = (LDS_DYN_MAX - base) // (16 * G * 4)
+    nsplit = max(-(-CUS // E), -(-te // max_tiles))
+    nsplit = max(1, min(nsplit, te))
+    tpw = -(-te // nsplit)
+    nsplit = -(-te // tpw)
+    return nsplit, tpw, base + tpw * 16 * G * 4 + 16  # + the kernel's static LDS
+
+
+def _routing(E, T, tk, kind, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "uniform":
+        ids = np.stack([rng.permutation(E)[:tk] for _ in range(T)])
+    else:
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        p /= p.sum()
+        ids = np.stack([rng.choice(E, tk, replace=False, p=p) for _ in range(T)])
+    return np.bincount(ids.ravel(), minlength=E)
+
+
+CASES = [
+    # E, H, I, T, tk, routing, layout (0 reference, 1 tiled), workgroups
+    (128, 2816, 704, 256, 8, "uniform", 1, (0, 77, 255)),
+    (128, 2816, 704, 1024, 8, "uniform", 0, (1, 128)),
+    (128, 2816, 704, 2048, 8, "zipf", 1, (0, 383, 767)),
+    (16, 256, 192, 64, 4, "uniform", 0, (0, 200)),
+    (2, 64, 1024, 64, 2, "uniform", 1, (0, 7)),
+]
+
+
+@pytest.mark.parametrize("E,H,I,T,tk,routing,layout,wgs", CASES)
+def test_down_kernel_addresses_and_register_flow(down_asm, E, H, I, T, tk, routing, layout, wgs):
+    G = I // 64
+    fn = f"_ZN3ksl12_GLOBAL__N_111down_kernelILi{G // 2}ELb{G % 2}ELi{layout}EEEvNS0_6DnArgsE"
+    ins, labels = emu.load_kernel(down_asm, fn)
+    counts = _routing(E, T, tk, routing, E + H + I)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    nrows = int(counts.sum())
+    nsplit, tpw, lds = _plan(E, H, I)
+    rb = 64 if nrows > 8192 else 0
+    grid = ((-(-nrows // rb) + E) if rb else E) * nsplit
+    bufs, base = {}, 0x7F0000000000
+
+    def alloc(name, size):
+        nonlocal base
+        bufs[name] = (base, base + size)
+        base += ((size + 0xFFFFF) // 0x100000 + 16) * 0x100000
+        return bufs[name][0]
+
+    p_out2 = alloc("out2", nrows * I * 2)
+    p_off = alloc("offsets", (E + 1) * 4)
+    p_q = alloc("dn_q", E * H * I // 2)
+    p_s = alloc("dn_s", E * H * G * 2)
+    p_z = alloc("dn_z", E * H * G * 2)
+    p_out3 = alloc("out3", nrows * H * 2)
+    p_karg = alloc("kernarg", 256)
+    # DnArgs, then the first hidden argument (the grid's block count)
+    karg = struct.pack("<QQQQQQiiiiii", p_out2, p_off, p_q, p_s, p_z, p_out3, H, I, nsplit, tpw, E, rb)
+    karg += struct.pack("<I", grid) + b"\0" * 60
+    mem = {p_karg + k: struct.unpack("<I", karg[k:k + 4])[0] for k in range(0, len(karg), 4)}
+    mem.update({p_off + 4 * e: int(offsets[e]) for e in range(E + 1)})
+    checked = 0
+    for wg in wgs:
+        assert wg < grid
+        shared = None
+        for wave_id in range(NW):
+            w = emu.Wave(mem, p_karg, wg, wave_id, bufs, lds)
+            if shared is not None:
+                w.lds = shared
+            emu.run(ins, labels, w)
+            shared = w.lds
+            checked += w.accesses
+            assert not w.errors, (wg, wave_id, w.errors[:4])
+    assert checked > 0
+
+
+SYNTHETIC = """synthetic:
+	global_load_dwordx4 v[4:7], v[0:1], off
+	v_mov_b64_e32 v[8:9], v[4:5]
+	s_waitcnt vmcnt(0)
+	global_load_dword v10, v[8:9], off
+	s_endpgm
+.Lfunc_end0:
+"""
+
+
+def test_emulator_flags_a_copied_in_flight_register(tmp_path):
+    """The hazard the checks above exclude, planted in a four-line kernel: a
+    loaded register copied before its wait and the copy used as an address."""
+    path = tmp_path / "syn.s"
+    path.write_text(SYNTHETIC)
+    ins, labels = emu.load_kernel(str(path), "synthetic")
+    buf = (0x7F0000000000, 0x7F0000100000)
+    w = emu.Wave({}, 0x7F0000200000, 0, 0, {"buf": buf, "karg": (0x7F0000200000, 0x7F0000200100)}, 1024)
+    w.v[0] = np.uint64(buf[0] & 0xFFFFFFFF) + np.arange(64, dtype=np.uint64) * np.uint64(16)
+    w.v[1] = np.uint64(buf[0] >> 32)
+    emu.run(ins, labels, w)
+    assert any(e[0] == "POISONED ADDRESS load" for e in w.errors), w.errors
