@@ -515,6 +515,41 @@ def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
     assert torch.equal(outs3[0].view(torch.int16), outs3[1].view(torch.int16))
 
 
+@pytest.mark.parametrize("E,H,I,T,zipf,layout", [(128, 2816, 704, 1200, 1.1, "tiled"), (128, 2816, 704, 1200, 1.1, "ref"),
+                                                 (64, 4096, 1024, 1100, None, "tiled"), (16, 512, 64, 2100, None, "ref")])
+def test_down_row_blocks_bit_equal_to_expert_mode(gpu, E, H, I, T, zipf, layout):
+    """Above 8192 routed rows down gives each workgroup a block of at most 64
+    rows of one expert (found through the routing offsets); below, a workgroup
+    walks all rows of its expert in 64-row chunks. Same out2 in, the same
+    out3 bits out, for the 64-K tail group (I = 704, I = 64), the largest I,
+    both weight layouts."""
+    lib = load_pkg()._lib
+    wl = load_mod("workloads")
+    v2 = load_mod("fused_moe_w4_v2")
+    L = lib.load()
+    tk = 8
+    ids, _ = wl.make_routing(T, E, tk, E + I, zipf)
+    counts = torch.bincount(ids.reshape(-1), minlength=E)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(counts, 0)]).to(torch.int32).to(gpu)
+    nrows = T * tk
+    assert nrows > 8192
+    exp = wl.make_experts(E, H, I, E + I + 1, device=gpu)
+    dn_q = v2.tiled_down(exp.dn_q) if layout == "tiled" else exp.dn_q
+    code = lib.DN_LAYOUT_TILED if layout == "tiled" else lib.DN_LAYOUT_REF
+    g = torch.Generator().manual_seed(E + I + 2)
+    out2 = (0.5 * torch.randn(nrows, I, generator=g)).to(torch.float16).to(gpu)
+    print(f"down row blocks E={E} H={H} I={I} rows {nrows} ({layout}) rows/expert max {int(counts.max())}", flush=True)
+    st = lib.stream_of(out2)
+    outs = []
+    for hint in (nrows, 100):  # row blocks, then one workgroup per expert
+        out3 = torch.full((nrows, H), float("nan"), dtype=torch.float16, device=gpu)
+        lib.check(L.ksl_moe_down(lib.ptr(out2), lib.ptr(offsets), lib.ptr(dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
+                                 E, H, I, hint, lib.ptr(out3), code, st), "ksl_moe_down")
+        outs.append(out3)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 @pytest.mark.parametrize("E,H,I", [(128, 4096, 1024), (256, 3072, 512)])
 def test_down_at_lds_limited_shapes(gpu, E, H, I):
     """The down launch at the contract's shapes whose column split is limited
