@@ -156,3 +156,12 @@ def test_emulator_flags_a_copied_in_flight_register(tmp_path):
     w.v[1] = np.uint64(buf[0] >> 32)
     emu.run(ins, labels, w)
     assert any(e[0] == "POISONED ADDRESS load" for e in w.errors), w.errors
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_down_kernel_every_width(down_asm, layout):
+    """Every instantiation of down_kernel (I = 64 .. 1024, with and without a
+    64-K tail group) on a small routing: one workgroup each, same checks."""
+    for G in range(1, 17):
+        I = 64 * G
+        test_down_kernel_addresses_and_register_flow(down_asm, 4, 128, I, 48, 2, "uniform", layout, (0, 5))
