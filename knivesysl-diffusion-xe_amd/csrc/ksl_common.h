@@ -344,6 +344,22 @@ __device__ __forceinline__ float act_times_up(float g, float u) {
     }
 }
 
+// act(g) * u with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32,
+// about 1 ulp each) instead of IEEE division: both forms are the logistic
+// function, g * sigmoid(g) and, since 0.5 * (1 + tanh(x)) = 1 / (1 + e^(-2x)),
+// the tanh-GELU. The fp32 differences are far below the fp16 rounding of
+// the stored value. Used where the epilogue's arithmetic shows in the time
+// (the row-block kernels of large routings).
+template <int ACT>
+__device__ __forceinline__ float act_times_up_fast(float g, float u) {
+    float z;
+    if (ACT == KSL_ACT_GELU_TANH)
+        z = -2.0f * 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    else
+        z = -g;
+    return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(z));
+}
+
 typedef __attribute__((address_space(3))) void* lds_vptr;
 typedef __attribute__((address_space(1))) void* gbl_vptr;
 
@@ -404,6 +420,76 @@ __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
+
+
+// ---- launch geometry shared by the expert GEMM kernels
+
+constexpr int kXcds = 8;
+
+// Index of the calling wave in its workgroup, in a scalar register (branches
+// on it are uniform).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
+
+// blockIdx.x -> logical tile, placing consecutive logical tiles on one XCD
+// (workgroups are dispatched round-robin over the XCDs).
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    if (nblocks % kXcds != 0) return bid;
+    return (bid % kXcds) * (nblocks / kXcds) + bid / kXcds;
+}
+
+// Row blocks (large routings): the rows of each expert split into blocks of at
+// most rb rows, numbered expert by expert (expert e has ceil(cnt_e / rb) of
+// them). The block `blk` of a workgroup is found by wave 0 from the offsets
+// (a wave scan of the per-expert block counts, 64 experts at a time) and
+// broadcast through LDS; every thread gets the same (e, start, M), M = 0
+// past the last block. One workgroup barrier, taken by every wave.
+__device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offsets, int E, int rb, int blk,
+                                               int& e, int& start, int& M) {
+    __shared__ int info[3];
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        if (lane == 0) {
+            info[0] = 0;
+            info[1] = 0;
+            info[2] = 0;
+        }
+        int base = 0;  // blocks of the experts before this batch
+        for (int e0 = 0; e0 < E; e0 += kWave) {
+            const int ex = e0 + lane;
+            int o0 = 0, cnt = 0;
+            if (ex < E) {
+                o0 = offsets[ex];
+                cnt = offsets[ex + 1] - o0;
+            }
+            const int nb = (cnt + rb - 1) / rb;
+            int incl = nb;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const int o = __shfl_up(incl, off, kWave);
+                if (lane >= off) incl += o;
+            }
+            const int excl = base + incl - nb;
+            if (ex < E && blk >= excl && blk < excl + nb) {
+                const int b = blk - excl;
+                info[0] = ex;
+                info[1] = o0 + b * rb;
+                info[2] = cnt - b * rb < rb ? cnt - b * rb : rb;
+            }
+            base += __shfl(incl, kWave - 1, kWave);
+        }
+    }
+    __syncthreads();
+    e = info[0];
+    start = info[1];
+    M = info[2];
+}
+
+// Buffer resource over `bytes` bytes at p (gfx9 raw buffer: stride 0, byte
+// offsets; a store at an offset past the end is dropped by the hardware).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
+}
+constexpr uint32_t kDropOffset = 0x80000000u;
 
 }  // namespace ksl
 

@@ -31,12 +31,11 @@
 //
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
-// rows (one or two 16-row M tiles); above 8192 routed rows one workgroup per
-// block of rows of an expert: 128-row blocks for gate/up (I % 176 == 0:
-// 128-row chunks, eight M tiles per decoded fragment), 64-row blocks for
-// down and for the other gate/up widths. Workgroups are remapped so that all
-// column blocks of an expert run on the same XCD (shared L2 for its
-// activations).
+// rows for gate/up (one or two 16-row M tiles) and 64 rows for down. Above
+// 8192 routed rows both GEMMs run the GEMM-form row-block kernels of
+// moe_rbgemm.hip instead. Workgroups are remapped so that all column blocks
+// of an expert run on the same XCD (shared L2 for its activations).
+
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -44,71 +43,20 @@
 #include "ksl_common.h"
 
 namespace ksl {
+
+// Row-block GEMM kernels of large routings (moe_rbgemm.hip).
+bool rb_gateup_fits(int64_t H, int64_t I);
+bool rb_down_fits(int64_t H, int64_t I);
+int launch_rb_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
+                     const uint8_t* gu_q, const void* gu_s, const void* gu_z, int64_t E, int64_t H, int64_t I,
+                     int act, void* out2, hipStream_t st, int64_t nrows);
+int launch_rb_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
+                   const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout,
+                   int64_t nrows);
+
 namespace {
 
-constexpr int kXcds = 8;
-constexpr int kRowBlock = 64;        // rows per workgroup block of a large routing
-constexpr int kRowBlockFrom = 8192;  // routed rows above which experts split into row blocks
-
-// Index of the calling wave in its workgroup, in a scalar register (branches
-// on it are uniform).
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
-
-// blockIdx.x -> logical tile, placing consecutive logical tiles on one XCD
-// (workgroups are dispatched round-robin over the XCDs).
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-    if (nblocks % kXcds != 0) return bid;
-    return (bid % kXcds) * (nblocks / kXcds) + bid / kXcds;
-}
-
-// Row blocks (large routings): the rows of each expert split into blocks of at
-// most rb rows, numbered expert by expert (expert e has ceil(cnt_e / rb) of
-// them). The block `blk` of a workgroup is found by wave 0 from the offsets
-// (a wave scan of the per-expert block counts, 64 experts at a time) and
-// broadcast through LDS; every thread gets the same (e, start, M), M = 0
-// past the last block. One workgroup barrier, taken by every wave.
-__device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offsets, int E, int rb, int blk,
-                                               int& e, int& start, int& M) {
-    __shared__ int info[3];
-    if (threadIdx.x < kWave) {
-        const int lane = threadIdx.x;
-        if (lane == 0) {
-            info[0] = 0;
-            info[1] = 0;
-            info[2] = 0;
-        }
-        int base = 0;  // blocks of the experts before this batch
-        for (int e0 = 0; e0 < E; e0 += kWave) {
-            const int ex = e0 + lane;
-            int o0 = 0, cnt = 0;
-            if (ex < E) {
-                o0 = offsets[ex];
-                cnt = offsets[ex + 1] - o0;
-            }
-            const int nb = (cnt + rb - 1) / rb;
-            int incl = nb;
-#pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                const int o = __shfl_up(incl, off, kWave);
-                if (lane >= off) incl += o;
-            }
-            const int excl = base + incl - nb;
-            if (ex < E && blk >= excl && blk < excl + nb) {
-                const int b = blk - excl;
-                info[0] = ex;
-                info[1] = o0 + b * rb;
-                info[2] = cnt - b * rb < rb ? cnt - b * rb : rb;
-            }
-            base += __shfl(incl, kWave - 1, kWave);
-        }
-    }
-    __syncthreads();
-    e = info[0];
-    start = info[1];
-    M = info[2];
-}
-
-
+constexpr int kRowBlockFrom = 8192;  // routed rows above which the row-block kernels run
 
 // ---------------------------------------------------------------- gate / up
 // One workgroup covers NC*16 columns of I of one expert (NC = 11: 176 columns,
@@ -129,8 +77,9 @@ __device__ __forceinline__ void find_row_block(const int32_t* __restrict__ offse
 constexpr int kMaxMt = 2;                        // 16-row M tiles per row chunk
 
 constexpr size_t kLdsBytes = 160 * 1024;         // LDS per workgroup on gfx950
-// Static LDS of these kernels (find_row_block's int[3]), rounded up; the
-// dynamic LDS of a launch is sized against what is left.
+// Static LDS reserved beside the dynamic LDS of a launch (these kernels
+// declare none today; the reserve keeps a helper with a small __shared__
+// array from pushing a launch sized to the limit over it).
 constexpr size_t kLdsStatic = 64;
 constexpr size_t kLdsDynMax = kLdsBytes - kLdsStatic;
 constexpr int kGuMaxG = 32;                      // H <= 4096
@@ -145,16 +94,14 @@ struct GuArgs {
     f16* out2;
     int topk, I, H;
     int early;  // producers issue the first weight groups before reading the routing
-    int E;
-    int rb;     // > 0: one workgroup per (block of rb rows of an expert, column block)
 };
 
-template <int NC, int NP, int R, int MX = kMaxMt>
+template <int NC, int NP, int R>
 struct GuShape {
     static constexpr int kCols = 16 * NC;                      // columns of I per workgroup
     static constexpr int kThreads = (NC + NP) * kWave;
     static constexpr int kSlotW = 2 * NC * kBlk;               // weight bytes per slot
-    static constexpr int kSlot = kSlotW + 4 * MX * kBlk;       // + activation bytes per slot (MX M tiles)
+    static constexpr int kSlot = kSlotW + 4 * kMaxMt * kBlk;   // + activation bytes per slot (two M tiles)
     static constexpr int kSzPer = (4 * kCols * kGuMaxG * 2 / 16 + NC * kWave - 1) / (NC * kWave);
     static constexpr size_t lds_bytes(int G) { return static_cast<size_t>(R) * kSlot + static_cast<size_t>(4) * kCols * G * 2; }
 };
@@ -166,9 +113,9 @@ struct GuShape {
 // Weight blocks of the first groups 0 .. min(R-1, G)-1 of a producer wave (the
 // blocks b = p + NP*k < 2*NC of gateup_produce), issued before the routing is
 // read: they do not depend on it.
-template <int NC, int NP, int R, int MX>
+template <int NC, int NP, int R>
 __device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int e, int c0, char* __restrict__ lds) {
-    using S = GuShape<NC, NP, R, MX>;
+    using S = GuShape<NC, NP, R>;
     const int lane = threadIdx.x & (kWave - 1);
     const int p = wave_id() - NC;
     const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
@@ -182,10 +129,10 @@ __device__ __forceinline__ void gateup_issue_first_weights(const GuArgs& A, int 
     }
 }
 
-template <int NC, int NP, int R, int MX, int MT>
+template <int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
                                                int m0, int mrows, bool w_issued) {
-    using S = GuShape<NC, NP, R, MX>;
+    using S = GuShape<NC, NP, R>;
     constexpr int NB = 2 * NC + 4 * MT;
     constexpr int KP = (NB + NP - 1) / NP;
     const int lane = threadIdx.x & (kWave - 1);
@@ -257,10 +204,10 @@ __device__ __forceinline__ void gateup_produce(const GuArgs& A, int e, int c0, c
 // a group from one wave, each address computed from a per-lane base (a wave
 // cannot keep one pointer per block in registers). Same slots, order and
 // barriers as gateup_produce.
-template <int NC, int R, int MX, int MT>
+template <int NC, int R, int MT>
 __device__ __forceinline__ void gateup_produce_1w(const GuArgs& A, int e, int c0, char* __restrict__ lds, int start,
                                                   int m0, int mrows, bool w_issued) {
-    using S = GuShape<NC, 1, R, MX>;
+    using S = GuShape<NC, 1, R>;
     constexpr int NB = 2 * NC + 4 * MT;
     const int lane = threadIdx.x & (kWave - 1);
     const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
@@ -318,10 +265,10 @@ __device__ __forceinline__ void gateup_produce_1w(const GuArgs& A, int e, int c0
 }
 
 // Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
-template <int ACT, int NC, int NP, int R, int MX, int MT>
+template <int ACT, int NC, int NP, int R, int MT>
 __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
                                                const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
-    using S = GuShape<NC, NP, R, MX>;
+    using S = GuShape<NC, NP, R>;
     const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
@@ -341,75 +288,40 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
         for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();  // group 0 and the scale table are ready
     int slot = 0;
-    // With up to four M tiles (MX > 2, the row blocks of large routings) the
-    // scale is folded into the B operand, b = fp16((q - z) * s), the
-    // reference's own dequantised weight, and the MFMAs accumulate into acc
-    // directly: two tiles' fp32 group partials would not fit the registers.
-    constexpr bool kFold = MX > 2;
     for (int g = 0; g < G; ++g) {
         const char* sp = lds + slot * S::kSlot;
-        f32x4 part[2][kFold ? 1 : MT];
-        if constexpr (!kFold) {
+        f32x4 part[2][MT];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+            for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         u32x4 wv[2];
         ZeroPair zc[2];
-        f16 sv[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             wv[j] = *reinterpret_cast<const u32x4*>(sp + (wave * 2 + j) * kBlk + fo);
             zc[j] = zero_pair((j ? z_u : z_g)[r * G + g]);
-            if constexpr (kFold) sv[j] = (j ? s_u : s_g)[r * G + g];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if constexpr (kFold && MT > 4) {
-                // eight M tiles: both decoded B fragments, then one activation
-                // fragment at a time (the accumulators take 64 registers)
-                f16x8 bb[2];
-#pragma unroll
-                for (int j = 0; j < 2; ++j) bb[j] = nib8_dequant(wv[j][i], zc[j], f16x2{sv[j], sv[j]}, kn);
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const f16x8 a1 = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
-                    acc[0][t] = mfma16x16x32(a1, bb[0], acc[0][t]);
-                    acc[1][t] = mfma16x16x32(a1, bb[1], acc[1][t]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                continue;
-            }
             f16x8 a[MT];
 #pragma unroll
             for (int t = 0; t < MT; ++t)
                 a[t] = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                if constexpr (kFold) {
-                    const f16x8 b = nib8_dequant(wv[j][i], zc[j], f16x2{sv[j], sv[j]}, kn);
+                const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
 #pragma unroll
-                    for (int t = 0; t < MT; ++t) acc[j][t] = mfma16x16x32(a[t], b, acc[j][t]);
-                } else {
-                    const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
-                }
+                for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
             }
-            // more than two M tiles: one 32-K step's fragments at a time
-            // (hoisting all four steps' activations would exceed 128 VGPRs)
-            if constexpr (MT > 2) __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (!kFold) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
+        for (int j = 0; j < 2; ++j) {
+            const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
 #pragma unroll
-                for (int t = 0; t < MT; ++t)
+            for (int t = 0; t < MT; ++t)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
-            }
+                for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
         }
         slot = slot + 1 == R ? 0 : slot + 1;
         __syncthreads();
@@ -431,30 +343,23 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
     }
 }
 
-template <int ACT, int NC, int NP, int R, int MX>
+template <int ACT, int NC, int NP, int R>
 __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A) {
-    using S = GuShape<NC, NP, R, MX>;
+    using S = GuShape<NC, NP, R>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     // Producer waves issue first on their SIMD after each barrier (the arbiter
     // otherwise favours the older consumer waves).
     if (wave_id() >= NC) __builtin_amdgcn_s_setprio(3);
     const int nb_per_e = A.I / S::kCols;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int unit = tile / nb_per_e;  // expert, or row block when A.rb > 0
-    const int c0 = (tile - unit * nb_per_e) * S::kCols;
-    int e, start, M;
-    if (A.rb > 0) {
-        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
-        if (M <= 0) return;  // past the last row block (uniform)
-    } else {
-        e = unit;
-        if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R, MX>(A, e, c0, lds);
-        start = A.offsets[e];
-        M = A.offsets[e + 1] - start;
-        if (M <= 0) {
-            vm_wait<0>();  // early weight loads land before the workgroup's LDS is released
-            return;
-        }
+    const int e = tile / nb_per_e;
+    const int c0 = (tile - e * nb_per_e) * S::kCols;
+    if (A.early && wave_id() >= NC) gateup_issue_first_weights<NC, NP, R>(A, e, c0, lds);
+    const int start = A.offsets[e];
+    const int M = A.offsets[e + 1] - start;
+    if (M <= 0) {
+        vm_wait<0>();  // early weight loads land before the workgroup's LDS is released
+        return;
     }
     const int G = A.H >> 7;
     const int tid = threadIdx.x;
@@ -462,27 +367,19 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     // Roles split once; both loops run the same chunks with the same barrier
     // count (1 + G per chunk), and the ring is free after a chunk's last barrier.
     if (wave_id() >= NC) {
-        for (int m0 = 0; m0 < M; m0 += 16 * MX) {
-            const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
+        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
+            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
             const bool w_issued = m0 == 0 && A.early;
             if constexpr (NP == 1) {
                 if (mrows <= 16)
-                    gateup_produce_1w<NC, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
-                else if (mrows <= 32)
-                    gateup_produce_1w<NC, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
-                else if (MX <= 4 || mrows <= 64)
-                    gateup_produce_1w<NC, R, MX, MX >= 4 ? 4 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                    gateup_produce_1w<NC, R, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
                 else
-                    gateup_produce_1w<NC, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
+                    gateup_produce_1w<NC, R, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
             } else {
                 if (mrows <= 16)
-                    gateup_produce<NC, NP, R, MX, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
-                else if (MX == 2 || mrows <= 32)
-                    gateup_produce<NC, NP, R, MX, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
-                else if (mrows <= 48)
-                    gateup_produce<NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, e, c0, lds, start, m0, mrows, w_issued);
+                    gateup_produce<NC, NP, R, 1>(A, e, c0, lds, start, m0, mrows, w_issued);
                 else
-                    gateup_produce<NC, NP, R, MX, MX>(A, e, c0, lds, start, m0, mrows, w_issued);
+                    gateup_produce<NC, NP, R, 2>(A, e, c0, lds, start, m0, mrows, w_issued);
             }
         }
     } else {
@@ -508,27 +405,12 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
                 if (i < 4 * nq) reinterpret_cast<u32x4*>(lds_sz)[i] = v[k];
             }
         }
-        for (int m0 = 0; m0 < M; m0 += 16 * MX) {
-            const int mrows = M - m0 < 16 * MX ? M - m0 : 16 * MX;
-            if constexpr (NP == 1) {
-                if (mrows <= 16)
-                    gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
-                else if (mrows <= 32)
-                    gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
-                else if (MX <= 4 || mrows <= 64)
-                    gateup_consume<ACT, NC, NP, R, MX, MX >= 4 ? 4 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
-                else
-                    gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
-            } else {
-                if (mrows <= 16)
-                    gateup_consume<ACT, NC, NP, R, MX, 1>(A, c0, lds, lds_sz, start, m0, mrows);
-                else if (MX == 2 || mrows <= 32)
-                    gateup_consume<ACT, NC, NP, R, MX, 2>(A, c0, lds, lds_sz, start, m0, mrows);
-                else if (mrows <= 48)
-                    gateup_consume<ACT, NC, NP, R, MX, MX >= 3 ? 3 : 2>(A, c0, lds, lds_sz, start, m0, mrows);
-                else
-                    gateup_consume<ACT, NC, NP, R, MX, MX>(A, c0, lds, lds_sz, start, m0, mrows);
-            }
+        for (int m0 = 0; m0 < M; m0 += 16 * kMaxMt) {
+            const int mrows = M - m0 < 16 * kMaxMt ? M - m0 : 16 * kMaxMt;
+            if (mrows <= 16)
+                gateup_consume<ACT, NC, NP, R, 1>(A, c0, lds, lds_sz, start, m0, mrows);
+            else
+                gateup_consume<ACT, NC, NP, R, 2>(A, c0, lds, lds_sz, start, m0, mrows);
         }
     }
 }
@@ -560,23 +442,22 @@ int device_cus() {
     return n;
 }
 
-template <int NC, int NP, int R, int MX = kMaxMt>
+template <int NC, int NP, int R>
 int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStream_t st) {
-    using S = GuShape<NC, NP, R, MX>;
-    // row blocks: at most ceil(nrows / rb) + E of them (one partial block per expert)
-    const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
-    if (units * (A.I / S::kCols) >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
-    const unsigned grid = static_cast<unsigned>(units * (A.I / S::kCols));
+    using S = GuShape<NC, NP, R>;
+    (void)nrows;
+    if (E * (A.I / S::kCols) >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    const unsigned grid = static_cast<unsigned>(E * (A.I / S::kCols));
     const size_t lds = S::lds_bytes(A.H / 128);
     if (lds > kLdsDynMax) return KSL_ERR_SHAPE;
     static const bool attr_set =
-        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R, MX>)) &&
-        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R, MX>));
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>)) &&
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>));
     (void)attr_set;
     if (act == KSL_ACT_GELU_TANH)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R, MX>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else if (act == KSL_ACT_SILU)
-        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R, MX>), dim3(grid), dim3(S::kThreads), lds, st, A);
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else
         return KSL_ERR_ARG;
     KSL_LAUNCH_CHECK();
@@ -626,8 +507,6 @@ struct DnArgs {
     const f16* dn_z;
     f16* out3;
     int H, I, nsplit, tpw;  // tpw: 16-column tiles per workgroup
-    int E;
-    int rb;                 // > 0: one workgroup per (block of rb rows of an expert, column split)
 };
 
 // LDS: activation blocks [kDnMaxMt][2G] (1 KB each, frag_pos order), then the
@@ -746,12 +625,6 @@ __device__ __forceinline__ void dn_stage_a(const DnArgs& A, char* a_lds, int sta
 }
 
 
-// Buffer resource over `bytes` bytes at p (gfx9 raw buffer: stride 0, byte
-// offsets; a store at an offset past the end is dropped by the hardware).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
-}
-constexpr uint32_t kDropOffset = 0x80000000u;
 
 // One tile: MT M tiles x 16 columns. The weights are the MFMA's A operand and
 // the activations its B operand, so the accumulator is the tile transposed:
@@ -823,16 +696,10 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
     constexpr int MTX = G2 >= 6 ? 2 : kDnMaxMt;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int unit = bid / A.nsplit;  // expert, or row block when A.rb > 0
-    const int h = bid - unit * A.nsplit;
-    int e, start, M;
-    if (A.rb > 0) {
-        find_row_block(A.offsets, A.E, A.rb, unit, e, start, M);
-    } else {
-        e = unit;
-        start = A.offsets[e];
-        M = A.offsets[e + 1] - start;
-    }
+    const int e = bid / A.nsplit;
+    const int h = bid - e * A.nsplit;
+    const int start = A.offsets[e];
+    const int M = A.offsets[e + 1] - start;
     const int col0 = h * A.tpw * 16;
     const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
     if (M <= 0 || ncols <= 0) return;
@@ -989,24 +856,19 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // with at least as many routed rows as experts most experts have rows: the
     // first weight groups go out before the routing is read
     A.early = nrows_hint >= E ? 1 : 0;
-    A.E = static_cast<int>(E);
-    // large routings: experts split into row blocks, so that a heavy expert
-    // (thousands of rows at prefill) spreads over many workgroups
-    A.rb = nrows_hint > kRowBlockFrom ? kRowBlock : 0;
-    if (A.rb > 0) A.early = 0;
+    // large routings (a heavy expert gets thousands of rows at prefill): the
+    // GEMM-form row-block kernel, 128-row blocks of each expert's rows
+    if (nrows_hint > kRowBlockFrom) {
+        if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+        if (!rb_gateup_fits(H, I)) return KSL_ERR_SHAPE;  // not reached within H <= 4096
+        return launch_rb_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st,
+                                nrows_hint);
+    }
     // widest column block that divides I: 176 (11 consumers), 128, or 64.
     // One workgroup per expert with 176 columns: 11 consumers and one
     // producer wave (12 waves, 3 per SIMD), ring depth 3
     if (I % 176 == 0) {
-        // row blocks (prefill): 128-row blocks and chunks, eight M tiles per
-        // decoded weight fragment, ring depth 2 (the slots hold 32 KB of
-        // activations); both shapes fit at the largest H (static_asserts)
-        static_assert(GuShape<11, 1, 2, 8>::lds_bytes(kGuMaxG) <= kLdsDynMax, "row-block gate/up LDS");
         static_assert(GuShape<11, 1, 3>::lds_bytes(kGuMaxG) <= kLdsDynMax, "gate/up LDS");
-        if (A.rb > 0) {
-            A.rb = 128;
-            return launch_gateup_nc<11, 1, 2, 8>(A, E, nrows_hint, act, st);
-        }
         return launch_gateup_nc<11, 1, 3>(A, E, nrows_hint, act, st);
     }
     if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, nrows_hint, act, st);
@@ -1052,14 +914,16 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     A.out3 = static_cast<f16*>(out3);
     A.H = static_cast<int>(H);
     A.I = static_cast<int>(I);
-    A.E = static_cast<int>(E);
-    A.rb = nrows > kRowBlockFrom ? kRowBlock : 0;
-    const int64_t units = A.rb > 0 ? (nrows + A.rb - 1) / A.rb + E : E;
+    // large routings: the GEMM-form row-block kernel (128-row blocks)
+    if (nrows > kRowBlockFrom) {
+        if (!rb_down_fits(H, I)) return KSL_ERR_SHAPE;  // not reached within the contract above
+        return launch_rb_down(out2, offsets, dn_q, dn_s, dn_z, E, H, I, out3, st, layout, nrows);
+    }
     const int G = static_cast<int>(I / 64);
     const DnPlan plan = plan_down(E, H, I, device_cus());
     A.tpw = static_cast<int>(plan.tpw);
     A.nsplit = static_cast<int>(plan.nsplit);
-    const int64_t grid = units * plan.nsplit;
+    const int64_t grid = E * plan.nsplit;
     if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
     const size_t lds = plan.lds;
     switch (G) {

@@ -280,22 +280,33 @@ def run(ins, labels, w, max_steps=2_000_000):
             if op.startswith("ds_write"):
                 if w.check_inflight_read(t[0]): w.errors.append(("POISONED ADDRESS ds", w.cur))
                 if any(w.check_inflight_read(x) for x in t[1:]): w.errors.append(("STALE DATA to LDS", w.cur))
-                nb = {"ds_write_b32": 4, "ds_write_b64": 8, "ds_write_b128": 16, "ds_write_b16": 2}[op]
+                nb = {"ds_write_b32": 4, "ds_write_b64": 8, "ds_write_b96": 12, "ds_write_b128": 16,
+                      "ds_write_b16": 2}[op]
                 off = 0
                 for x in t[2:]:
                     if x.startswith("offset:"): off = int(x[7:], 0)
-                a, ka = w.vget(t[0]); d, kd = w.vget(t[1], nb // 4 if nb >= 4 else 1)
+                a, ka = w.vget(t[0])
+                # data dword by dword (a uint64 lane value holds two)
+                dr = w.vreg(t[1])
+                nd = max(1, nb // 4)
+                if dr is not None:
+                    dws = [(w.v[i], w.vk[i]) for i in dr[:nd]]
+                else:
+                    d0, k0 = w.vget(t[1]); dws = [(d0, k0)]
                 act = w.act()
                 for l in range(NL):
                     if not act[l]: continue
                     if not ka[l]: w.errors.append(("ds_write unknown address", w.cur)); break
                     base = int(a[l]) + off
                     if base + nb > w.lds_size: w.errors.append(("ds_write beyond LDS", base, w.cur))
-                    val = int(d[l])
-                    for b in range(nb): w.lds[base + b] = ((val >> (8 * b)) & 0xFF, bool(kd[l]))
+                    for b in range(nb):
+                        dv, dk = dws[min(b // 4, len(dws) - 1)]
+                        w.lds[base + b] = ((int(dv[l]) >> (8 * (b % 4))) & 0xFF, bool(dk[l]))
                 continue
-            if op in ("ds_read_b32", "ds_read_b64", "ds_read_u16", "ds_read_b128", "ds_read_u8", "ds_bpermute_b32"):
-                nb = {"ds_read_b32": 4, "ds_read_b64": 8, "ds_read_u16": 2, "ds_read_b128": 16, "ds_read_u8": 1, "ds_bpermute_b32": 4}[op]
+            if op in ("ds_read_b32", "ds_read_b64", "ds_read_b96", "ds_read_u16", "ds_read_b128", "ds_read_u8",
+                      "ds_bpermute_b32"):
+                nb = {"ds_read_b32": 4, "ds_read_b64": 8, "ds_read_b96": 12, "ds_read_u16": 2, "ds_read_b128": 16,
+                      "ds_read_u8": 1, "ds_bpermute_b32": 4}[op]
                 off = 0
                 for x in t[2:]:
                     if x.startswith("offset:"): off = int(x[7:], 0)

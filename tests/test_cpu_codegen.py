@@ -9,8 +9,10 @@ down_kernel are run through tests/gfx950_emu.py: every global, buffer and LDS
 access must stay in its buffer and no address, stored value or MFMA operand
 may come from a register whose load had not landed. Shapes: the 256-token
 layer (one chunk, up to two M tiles), 1024 tokens (four M tiles, several
-chunks per expert), a Zipf routing above 8192 rows (row blocks found through
-LDS), and small / odd I (a 64-K tail group, the largest I)."""
+chunks per expert), a Zipf routing of 1024 tokens (experts of a few to many
+chunks), and small / odd I (a 64-K tail group, the largest I). Above 8192
+routed rows a different kernel runs (moe_rbgemm.hip), whose weights go
+through LDS by direct loads and ordinary register loads only."""
 from __future__ import annotations
 
 import importlib.util
@@ -50,8 +52,8 @@ def down_asm(tmp_path_factory):
     return out
 
 
-# The launch plan of csrc/moe_gemm.hip (plan_down, kDnWaves, kDnMaxMt, the
-# row-block threshold) restated for the emulated launches.
+# The launch plan of csrc/moe_gemm.hip (plan_down, kDnWaves, kDnMaxMt)
+# restated for the emulated launches.
 NW, MAX_MT, LDS_DYN_MAX, CUS = 12, 4, 160 * 1024 - 64, 256
 
 
@@ -64,7 +66,7 @@ def _plan(E, H, I):
     nsplit = max(1, min(nsplit, te))
     tpw = -(-te // nsplit)
     nsplit = -(-te // tpw)
-    return nsplit, tpw, base + tpw * 16 * G * 4 + 16  # + the kernel's static LDS
+    return nsplit, tpw, base + tpw * 16 * G * 4
 
 
 def _routing(E, T, tk, kind, seed):
@@ -82,7 +84,7 @@ CASES = [
     # E, H, I, T, tk, routing, layout (0 reference, 1 tiled), workgroups
     (128, 2816, 704, 256, 8, "uniform", 1, (0, 77, 255)),
     (128, 2816, 704, 1024, 8, "uniform", 0, (1, 128)),
-    (128, 2816, 704, 2048, 8, "zipf", 1, (0, 383, 767)),
+    (128, 2816, 704, 1024, 8, "zipf", 1, (6, 7, 255)),
     (16, 256, 192, 64, 4, "uniform", 0, (0, 200)),
     (2, 64, 1024, 64, 2, "uniform", 1, (0, 7)),
 ]
@@ -97,8 +99,8 @@ def test_down_kernel_addresses_and_register_flow(down_asm, E, H, I, T, tk, routi
     offsets = np.concatenate([[0], np.cumsum(counts)])
     nrows = int(counts.sum())
     nsplit, tpw, lds = _plan(E, H, I)
-    rb = 64 if nrows > 8192 else 0
-    grid = ((-(-nrows // rb) + E) if rb else E) * nsplit
+    assert nrows <= 8192  # larger routings run the row-block kernels
+    grid = E * nsplit
     bufs, base = {}, 0x7F0000000000
 
     def alloc(name, size):
@@ -115,7 +117,7 @@ def test_down_kernel_addresses_and_register_flow(down_asm, E, H, I, T, tk, routi
     p_out3 = alloc("out3", nrows * H * 2)
     p_karg = alloc("kernarg", 256)
     # DnArgs, then the first hidden argument (the grid's block count)
-    karg = struct.pack("<QQQQQQiiiiii", p_out2, p_off, p_q, p_s, p_z, p_out3, H, I, nsplit, tpw, E, rb)
+    karg = struct.pack("<QQQQQQiiii", p_out2, p_off, p_q, p_s, p_z, p_out3, H, I, nsplit, tpw)
     karg += struct.pack("<I", grid) + b"\0" * 60
     mem = {p_karg + k: struct.unpack("<I", karg[k:k + 4])[0] for k in range(0, len(karg), 4)}
     mem.update({p_off + 4 * e: int(offsets[e]) for e in range(E + 1)})

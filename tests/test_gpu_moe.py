@@ -281,6 +281,10 @@ STAGE_CASES = [
     (192, 2, 3, 256, 1024, 39),   # the largest I (16 64-groups)
     (1100, 8, 12, 256, 768, 40),  # 8800 rows: row blocks with I >= 768
     (8, 8, 128, 2816, 704, 41),   # 64 rows over 128 experts: most experts empty, one producer without early issue
+    # above 8192 rows, the GEMM-form row-block kernels (128-row blocks, full and partial)
+    (1040, 8, 64, 2816, 704, 42),  # the layer's H and I: 6 down column blocks (the last half full), 64-K tail
+    (1100, 8, 8, 384, 128, 43),    # three 128-groups of gate/up, one down group, 4 of 8 gate/up waves active
+    (1100, 8, 8, 256, 64, 44),     # down is only the 64-K tail group, 2 of 8 gate/up waves active
 ]
 
 
@@ -480,13 +484,12 @@ def test_tiled_down_forward_is_bit_identical(gpu, T, tk, E, H, I, seed):
 @pytest.mark.parametrize("T,tk,E,H,I,zipf,seed", [(1200, 8, 16, 256, 128, None, 91), (2048, 8, 128, 512, 256, 1.1, 92)])
 def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
     """Above 8192 routed rows gate/up and down give each workgroup a block of
-    at most 128 rows of one expert. At the 128- and 64-column gate/up shapes
-    run here (I = 128, 256) both modes use the same decode, so the gate/up and
-    down outputs equal the one-workgroup-per-expert mode (selected by a small
-    row count) bit for bit. At I = 704 the row-block gate/up multiplies the
-    fp16-dequantised weights instead (the reference's rounding), so its bits
-    differ from the small-routing form; that case (8800 rows) is compared with
-    the oracle on every row by test_gateup_and_down_stages."""
+    at most 128 rows of one expert (the GEMM-form kernels of
+    csrc/moe_rbgemm.hip). Down: the same out2 gives the same out3 bits in both
+    modes. Gate/up: the row-block kernel multiplies the fp16-dequantised
+    weights (the reference's rounding) while the per-expert kernel takes the
+    exact integers (q - z) with an fp32 group scale, so their bits differ;
+    both are compared with the oracle on every row."""
     lib = load_pkg()._lib
     wl = load_mod("workloads")
     L = lib.load()
@@ -499,30 +502,37 @@ def test_row_blocks_match_expert_mode(gpu, T, tk, E, H, I, zipf, seed):
     print(f"row blocks T={T} E={E} rows/expert {int(counts.min())}..{int(counts.max())}", flush=True)
     st = lib.stream_of(a16)
     outs2, outs3 = [], []
-    for t_hint, nrows in ((T, T * tk), (1, 100)):   # row blocks, then one workgroup per expert
+    for t_hint in (T, 1):   # row blocks, then one workgroup per expert
         out2 = torch.empty(T * tk, I, dtype=torch.float16, device=gpu)
-        out3 = torch.empty(T * tk, H, dtype=torch.float16, device=gpu)
         rc = L.ksl_moe_gateup_act(lib.ptr(a16), lib.ptr(sr), lib.ptr(off), t_hint, tk, lib.ptr(exp.gu_q),
                                   lib.ptr(exp.gu_s), lib.ptr(exp.gu_z), E, H, I, lib.ACT_SILU, lib.ptr(out2), st)
         lib.check(rc, "ksl_moe_gateup_act")
-        rc = L.ksl_moe_down(lib.ptr(out2), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
+        outs2.append(out2)
+    for nrows in (T * tk, 100):   # the row-block kernel's out2 into both down modes
+        out3 = torch.full((T * tk, H), float("nan"), dtype=torch.float16, device=gpu)
+        rc = L.ksl_moe_down(lib.ptr(outs2[0]), lib.ptr(off), lib.ptr(exp.dn_q), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z),
                             E, H, I, nrows, lib.ptr(out3), lib.DN_LAYOUT_REF, st)
         lib.check(rc, "ksl_moe_down")
-        outs2.append(out2)
         outs3.append(out3)
     torch.cuda.synchronize()
-    assert torch.equal(outs2[0].view(torch.int16), outs2[1].view(torch.int16))
     assert torch.equal(outs3[0].view(torch.int16), outs3[1].view(torch.int16))
+    gu_q, gu_s, gu_z, dn_q, dn_s, dn_z = [_np(getattr(exp, k)) for k in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z")]
+    _, ref_out2, _ = mo.moe_forward_per_expert(hidden.float().numpy(), gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
+                                                ids.numpy(), np.ones((T, tk), np.float32), mo.ACT_SILU)
+    inv_np = _np(inv).astype(np.int64)
+    for mode, o2 in zip(("row blocks", "per expert"), outs2):
+        got = out2_unperm(_np(o2), I)[inv_np]
+        check_norm_err("gateup", got.astype(np.float32), ref_out2.astype(np.float32), f"{mode} T={T} E={E} I={I}")
 
 
 @pytest.mark.parametrize("E,H,I,T,zipf,layout", [(128, 2816, 704, 1200, 1.1, "tiled"), (128, 2816, 704, 1200, 1.1, "ref"),
                                                  (64, 4096, 1024, 1100, None, "tiled"), (16, 512, 64, 2100, None, "ref")])
 def test_down_row_blocks_bit_equal_to_expert_mode(gpu, E, H, I, T, zipf, layout):
-    """Above 8192 routed rows down gives each workgroup a block of at most 64
-    rows of one expert (found through the routing offsets); below, a workgroup
-    walks all rows of its expert in 64-row chunks. Same out2 in, the same
-    out3 bits out, for the 64-K tail group (I = 704, I = 64), the largest I,
-    both weight layouts."""
+    """Above 8192 routed rows down gives each workgroup a block of at most 128
+    rows of one expert (found through the routing offsets; GEMM-form kernel);
+    below, a workgroup walks all rows of its expert in 64-row chunks. Same
+    out2 in, the same out3 bits out, for the 64-K tail group (I = 704,
+    I = 64), the largest I, both weight layouts."""
     lib = load_pkg()._lib
     wl = load_mod("workloads")
     v2 = load_mod("fused_moe_w4_v2")
