@@ -285,6 +285,8 @@ STAGE_CASES = [
     (1040, 8, 64, 2816, 704, 42),  # the layer's H and I: 6 down column blocks (the last half full), 64-K tail
     (1100, 8, 8, 384, 128, 43),    # three 128-groups of gate/up, one down group, 4 of 8 gate/up waves active
     (1100, 8, 8, 256, 64, 44),     # down is only the 64-K tail group, 2 of 8 gate/up waves active
+    (1100, 8, 8, 4096, 128, 45),   # the largest H: 32 scale groups per gate/up row, 16 down column blocks
+    (1100, 8, 512, 256, 64, 46),   # 512 experts of ~17 rows: partial row blocks, the block search over 8 batches
 ]
 
 
