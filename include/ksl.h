@@ -39,6 +39,9 @@ extern "C" {
 /* activation codes for the gate/up epilogue */
 #define KSL_ACT_GELU_TANH 0 /* kernels/fused_moe_w4_v2.py:136-138 */
 #define KSL_ACT_SILU 1      /* SiLU-gated variant (act(g) = g * sigmoid(g)) */
+#define KSL_ACT_NONE 2      /* ksl_moe_gateup_act only: gate and up themselves, no
+                             * activation (the v1 path, kernels/fused_moe_w4.py:117-119);
+                             * the forwards reject it */
 
 /* layouts of the down weights dn_q */
 #define KSL_DN_LAYOUT_REF 0   /* [E, H, I/2] as packed (kernels/w4a16.py:19-32) */
@@ -73,6 +76,24 @@ int ksl_rmsnorm(const void* x, int x_dtype, const void* w, int w_dtype, void* y,
  * as dropped (the reference raises an index error there). E <= 512. */
 int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
                   int64_t* sorted_rows, int64_t* expert_ids, int64_t* inv, void* stream);
+
+/* Routing metadata in the int32 token-row form, one launch.
+ * Replaces moe_align_cuda (kernels/fused_moe_w4_v2.py:46-76: marlin's
+ * moe_align_block_size followed by _align_finalize, :32-43):
+ *   a_row      int32[cap]   token (expanded row / topk) of each sorted slot,
+ *                           padding slots = T
+ *   expert_ids int32[cap / block_m]  expert of each block, padding = E
+ *   inv        int32[T*topk] sorted slot of each expanded row
+ * cap = ksl_moe_align_i32_capacity(T, topk, E, block_m), the reference's
+ * mx = T*topk + E*(block_m-1) (min(T*topk*block_m, mx) when T*topk < E)
+ * rounded up to whole blocks. Rows of an expert keep their expanded-row
+ * order (the reference's marlin kernel places them in an unspecified order;
+ * every consumer of the layout is indifferent to it). Ids must lie in
+ * [0, E) as the reference's contract requires (:48-56); an id outside is
+ * treated as dropped (inv 0, no slot). E <= 512. */
+int64_t ksl_moe_align_i32_capacity(int64_t T, int64_t topk, int64_t E, int64_t block_m);
+int ksl_moe_align_i32(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
+                      int32_t* a_row, int32_t* expert_ids, int32_t* inv, void* stream);
 
 /* Workspace bytes the fused forward needs for these shapes: the routing
  * (sorted rows, offsets, inv), the fp16 activations, out2, out3 and the
@@ -190,7 +211,11 @@ int ksl_moe_route(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
  * stored at i*32 + c*8 + s(j). T: the tokens of a16 (T*topk routed rows;
  * with at least E of them the first weight groups are fetched before the
  * routing is read; above 8192 of them each workgroup takes a block of at most
- * 64 rows of one expert). */
+ * 64 rows of one expert).
+ * act KSL_ACT_NONE (the v1 grouped GEMM, kernels/fused_moe_w4.py:54-90 as
+ * fused_moe_w4 runs it on gate/up, :117-118): out2 is instead out1 fp16
+ * [T*topk, 2I], gate in columns 0..I-1 and up in I..2I-1, plain column order,
+ * no activation; every routing size runs the per-expert kernel. */
 int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_t* offsets,
                        int64_t T, int64_t topk, const uint8_t* gu_q, const void* gu_s, const void* gu_z,
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
@@ -204,6 +229,13 @@ int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_
 int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
                  const void* dn_z, int64_t E, int64_t H, int64_t I, int64_t nrows, void* out3, int dn_layout,
                  void* stream);
+
+/* Activation rows fp16 [rows, I] in plain column order (what an activation
+ * applied outside the kernels writes, kernels/fused_moe_w4.py:119) -> the same
+ * rows in the down activation order of ksl_moe_gateup_act's out2, ready for
+ * ksl_moe_down. No reference counterpart: the v1 path's glue. src != dst,
+ * both 16-byte aligned, I % 64 == 0. */
+int ksl_moe_act_to_down_order(const void* src, int64_t rows, int64_t I, void* dst, void* stream);
 
 /* Dynamic LDS bytes a ksl_moe_down launch requests for an (E, H, I) layer on
  * a device with cus compute units (host-only arithmetic, no device call; 0
@@ -301,6 +333,14 @@ int ksl_moe_pack_down(const uint8_t* dn_q, const void* dn_s, const void* dn_z, i
 int ksl_moe_combine(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
                     int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
                     void* stream);
+
+/* The v1 combine (kernels/fused_moe_w4.py:125-127, (out3[inv].view(T, topk, H)
+ * * topk_w.to(fp16)).sum(1).to(y dtype)): per slot k in order, the product
+ * fp16(fp16(w[t,k]) * out3[inv[t*topk+k], :]) summed in fp32, the sum rounded
+ * to fp16, then to y_dtype. Arguments as ksl_moe_combine. */
+int ksl_moe_combine_v1(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                       int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
+                       void* stream);
 
 /* Expert router, the step before the MoE: TF modeling_diffusion_gemma.py:529-548
  * (DiffusionGemmaTextRouter.forward), its scale-free norm being the fused

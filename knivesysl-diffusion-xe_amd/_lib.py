@@ -15,7 +15,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libksl.so")
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-ACT_GELU_TANH, ACT_SILU = 0, 1
+ACT_GELU_TANH, ACT_SILU, ACT_NONE = 0, 1, 2
 DN_LAYOUT_REF, DN_LAYOUT_TILED = 0, 1
 ERR_SCRATCH, ERR_RUNTIME = 6, 7
 NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
@@ -37,6 +37,8 @@ SIGNATURES = {
     "ksl_status_string": ([_I], ctypes.c_char_p),
     "ksl_rmsnorm": ([_P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _F, _P], _I),
     "ksl_moe_align": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
+    "ksl_moe_align_i32_capacity": ([_I64, _I64, _I64, _I64], _I64),
+    "ksl_moe_align_i32": ([_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_workspace_bytes": ([_I64, _I64, _I64, _I64, _I64], _SZ),
     "ksl_moe_w4a16_forward": ([_P, _I, _I64, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
@@ -48,6 +50,8 @@ SIGNATURES = {
     "ksl_moe_unshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
+    "ksl_moe_combine_v1": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
+    "ksl_moe_act_to_down_order": ([_P, _I64, _I64, _P, _P], _I),
     "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
     "ksl_moe_layer_forward_noalloc": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,

@@ -42,7 +42,10 @@ constexpr int kCombThreads = 256;
 // acc[j] = sum over slots k in order of fp32(w[t,k]) * fp32(out3[inv[t*topk+k], c0+j]).
 // 8 slots at a time: all index/weight loads (uniform per token), then all row
 // loads (clamped slot index: one round trip each), then the FMA chain in slot order.
-template <int WD>
+// F16P (the v1 combine, kernels/fused_moe_w4.py:125-127): the weight is
+// rounded to fp16 first and each product w * x to fp16 (torch's fp16 multiply),
+// the products are summed in fp32 in slot order.
+template <int WD, bool F16P = false>
 __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const int32_t* __restrict__ inv,
                                             const typename Elem<WD>::T* __restrict__ w, int64_t t, int topk,
                                             int64_t H, int64_t c0, float (&acc)[8]) {
@@ -56,6 +59,7 @@ __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const 
             const int kk = k0 + k < topk ? k0 + k : topk - 1;
             r[k] = inv[t * topk + kk];
             wk[k] = Elem<WD>::load(w + t * topk + kk);
+            if (F16P) wk[k] = static_cast<float>(static_cast<f16>(wk[k]));
         }
         f16x8 x[8];
 #pragma unroll
@@ -64,13 +68,18 @@ __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const 
         for (int k = 0; k < 8; ++k) {
             if (k0 + k < topk) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(wk[k], static_cast<float>(x[k][j]), acc[j]);
+                for (int j = 0; j < 8; ++j) {
+                    if (F16P)
+                        acc[j] += static_cast<float>(static_cast<f16>(wk[k] * static_cast<float>(x[k][j])));
+                    else
+                        acc[j] = __builtin_fmaf(wk[k], static_cast<float>(x[k][j]), acc[j]);
+                }
             }
         }
     }
 }
 
-template <int WD, int YD>
+template <int WD, int YD, bool F16P>
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __restrict__ out3,
                                                               const int32_t* __restrict__ inv,
                                                               const void* __restrict__ wv, int64_t T,
@@ -84,11 +93,15 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
     if (t >= T) return;
     const int64_t c0 = (idx - t * hv) * 8;
     float acc[8];
-    combine_acc<WD>(out3, inv, static_cast<const typename Elem<WD>::T*>(wv), t, topk, H, c0, acc);
+    combine_acc<WD, F16P>(out3, inv, static_cast<const typename Elem<WD>::T*>(wv), t, topk, H, c0, acc);
+    if (F16P) {  // the fp16 sum, then .to(y dtype)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = static_cast<float>(static_cast<f16>(acc[j]));
+    }
     store8<YD>(y + t * ys + c0, acc);
 }
 
-template <int WD>
+template <int WD, bool F16P>
 int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w, int64_t T,
                      int64_t topk, int64_t H, void* y, int64_t ys, hipStream_t st) {
     const int64_t n = T * (H / 8);
@@ -96,15 +109,15 @@ int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w
     const f16* o3 = static_cast<const f16*>(out3);
     switch (yd) {
         case KSL_DTYPE_BF16:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_BF16>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_BF16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
                                inv, w, T, static_cast<int>(topk), H, y, ys);
             break;
         case KSL_DTYPE_F16:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F16>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
                                inv, w, T, static_cast<int>(topk), H, y, ys);
             break;
         case KSL_DTYPE_F32:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F32>), dim3(grid), dim3(kCombThreads), 0, st, o3,
+            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F32, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
                                inv, w, T, static_cast<int>(topk), H, y, ys);
             break;
         default:
@@ -209,16 +222,24 @@ __global__ __launch_bounds__(kPostMaxWaves * kWave) void combine_post_kernel(Pos
 }  // namespace
 
 int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
-                   int64_t topk, int64_t H, void* y, int yd, int64_t ys, hipStream_t st) {
+                   int64_t topk, int64_t H, void* y, int yd, int64_t ys, hipStream_t st, bool f16p = false) {
     if (!out3 || !inv || !w || !y) return T == 0 ? KSL_OK : KSL_ERR_ARG;
     if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0 || ys < H) return KSL_ERR_SHAPE;
     if (ys % 8 != 0 || reinterpret_cast<uintptr_t>(out3) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
         return KSL_ERR_ALIGN;
     if (T == 0) return KSL_OK;
+    if (f16p) {
+        switch (wd) {
+            case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
+            case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
+            case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        }
+        return KSL_ERR_ARG;
+    }
     switch (wd) {
-        case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32>(yd, out3, inv, w, T, topk, H, y, ys, st);
-        case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16>(yd, out3, inv, w, T, topk, H, y, ys, st);
-        case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
     }
     return KSL_ERR_ARG;
 }
@@ -331,6 +352,13 @@ extern "C" int ksl_moe_combine(const void* out3, const int32_t* inv, const void*
                                int64_t y_stride, void* stream) {
     return ksl::launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride,
                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ksl_moe_combine_v1(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
+                                  int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
+                                  void* stream) {
+    return ksl::launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride,
+                               static_cast<hipStream_t>(stream), true);
 }
 
 extern "C" int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,

@@ -327,7 +327,21 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
         __syncthreads();
     }
     // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
-    {
+    if (ACT == KSL_ACT_NONE) {
+        // gate and up themselves, fp16, in plain column order: out1 [rows, 2I]
+        const int64_t ld = 2 * static_cast<int64_t>(A.I);
+        f16* o = A.out2 + (static_cast<int64_t>(start + m0) + 4 * c) * ld + c0 + wave * 16 + col;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = t * 16 + 4 * c + q;
+                if (row < mrows) {
+                    o[(t * 16 + q) * ld] = static_cast<f16>(acc[0][t][q]);
+                    o[(t * 16 + q) * ld + A.I] = static_cast<f16>(acc[1][t][q]);
+                }
+            }
+    } else {
         const int sc = out2_store_index(c0 + wave * 16 + col, A.I & ~127);  // out2 is the down GEMM's activation
         // the lane's part of the row offset (4c rows) in its pointer, the
         // uniform part ((16t + q) rows) as a scalar offset
@@ -452,12 +466,15 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
     if (lds > kLdsDynMax) return KSL_ERR_SHAPE;
     static const bool attr_set =
         set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>)) &&
-        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>));
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>)) &&
+        set_max_lds(reinterpret_cast<const void*>(&gateup_act_kernel<KSL_ACT_NONE, NC, NP, R>));
     (void)attr_set;
     if (act == KSL_ACT_GELU_TANH)
         hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_GELU_TANH, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else if (act == KSL_ACT_SILU)
         hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_SILU, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
+    else if (act == KSL_ACT_NONE)
+        hipLaunchKernelGGL((gateup_act_kernel<KSL_ACT_NONE, NC, NP, R>), dim3(grid), dim3(S::kThreads), lds, st, A);
     else
         return KSL_ERR_ARG;
     KSL_LAUNCH_CHECK();
@@ -830,6 +847,22 @@ __global__ __launch_bounds__(256) void unshuffle_ns_down_kernel(const uint8_t* _
     *reinterpret_cast<uint64_t*>(out + (static_cast<int64_t>(e) * H + nt * 64 + n) * ih + kb * 32 + 8 * m) = v;
 }
 
+// Activation rows in plain column order -> the down kernel's activation
+// order (out2_store_index): thread i moves 8 consecutive columns of one row.
+__global__ __launch_bounds__(256) void act_to_down_order_kernel(const f16* __restrict__ src, int64_t rows, int I,
+                                                                f16* __restrict__ dst) {
+    const int64_t n8 = I / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= rows * n8) return;
+    const int64_t r = idx / n8;
+    const int n0 = static_cast<int>(idx - r * n8) * 8;
+    const f16x8 v = *reinterpret_cast<const f16x8*>(src + r * I + n0);
+    f16* o = dst + r * I;
+    const int i128 = I & ~127;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[out2_store_index(n0 + j, i128)] = v[j];
+}
+
 }  // namespace
 
 int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t topk,
@@ -858,8 +891,9 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     A.early = nrows_hint >= E ? 1 : 0;
     // large routings (a heavy expert gets thousands of rows at prefill): the
     // GEMM-form row-block kernel, 128-row blocks of each expert's rows
-    if (nrows_hint > kRowBlockFrom) {
-        if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU) return KSL_ERR_ARG;
+    if (act != KSL_ACT_GELU_TANH && act != KSL_ACT_SILU && act != KSL_ACT_NONE) return KSL_ERR_ARG;
+    // (gate and up without the activation: the per-expert kernel at every size)
+    if (nrows_hint > kRowBlockFrom && act != KSL_ACT_NONE) {
         if (!rb_gateup_fits(H, I)) return KSL_ERR_SHAPE;  // not reached within H <= 4096
         return launch_rb_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2, st,
                                 nrows_hint);
@@ -944,6 +978,21 @@ extern "C" int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, c
                                   int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream) {
     return ksl::launch_gateup(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, E, H, I, act, out2,
                               static_cast<hipStream_t>(stream), T > 0 ? T * topk : 0);
+}
+
+extern "C" int ksl_moe_act_to_down_order(const void* src, int64_t rows, int64_t I, void* dst, void* stream) {
+    using namespace ksl;
+    if (rows < 0 || I <= 0 || I % 64 != 0 || I > (int64_t(1) << 20)) return KSL_ERR_SHAPE;
+    if (rows == 0) return KSL_OK;
+    if (!src || !dst || src == dst) return KSL_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16) return KSL_ERR_ALIGN;
+    const int64_t n = rows * (I / 8);
+    if ((n + 255) / 256 >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    hipLaunchKernelGGL(act_to_down_order_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(src), rows, static_cast<int>(I),
+                       static_cast<f16*>(dst));
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
 }
 
 extern "C" int ksl_moe_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q,

@@ -77,6 +77,10 @@ struct RouteOut {
     int E;
     int32_t* zero;  // counters cleared by the routing (the expert FFN's), kCtlStride words apart, or null
     int nzero;
+    // token-row mode (the moe_align_cuda contract): a real slot holds its
+    // token r / row_div instead of the expanded row r, a padding slot pad_tok
+    // (T) instead of Nexp. row_div == 0: expanded rows.
+    int64_t row_div = 0, pad_tok = 0;
 };
 
 // Clear the n counters (kCtlStride words apart) a following launch expects
@@ -319,6 +323,7 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
                            int32_t* __restrict__ offsets) {
     const int64_t Nexp = R.Nexp, cap = R.cap, max_blocks = R.max_blocks, block_m = R.block_m;
     const int E = R.E;
+    const IdxT pad_row = static_cast<IdxT>(R.row_div ? R.pad_tok : Nexp);
     extern __shared__ int32_t lds[];
     int32_t* wcnt = lds;                                  // [kRouteWaves][E]
     int64_t* estart = reinterpret_cast<int64_t*>(lds + kRouteWaves * E);  // [E], 8-byte aligned (16*E ints)
@@ -393,7 +398,7 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
     if (e < E) {
         if (sorted_rows) {
             for (int64_t p = blk_start * block_m + cnt; p < (blk_start + nblk) * block_m; ++p)
-                sorted_rows[p] = static_cast<IdxT>(Nexp);
+                sorted_rows[p] = pad_row;
         }
         if (expert_ids) {
             for (int64_t b = blk_start; b < blk_start + nblk; ++b) expert_ids[b] = static_cast<IdxT>(e);
@@ -404,7 +409,7 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
     if (R.zero) clear_words(R.zero, R.nzero, threadIdx.x, kRouteThreads);
     if (sorted_rows) {
         for (int64_t p = tot_blocks * block_m + threadIdx.x; p < cap; p += kRouteThreads)
-            sorted_rows[p] = static_cast<IdxT>(Nexp);
+            sorted_rows[p] = pad_row;
     }
     if (expert_ids) {
         for (int64_t b = tot_blocks + threadIdx.x; b < max_blocks; b += kRouteThreads)
@@ -424,7 +429,7 @@ __device__ void route_block(const int64_t* __restrict__ ids, const RouteOut& R, 
                 if (key < E) {
                     const int32_t before = mycnt[key];
                     const int64_t slot = estart[key] + before + __builtin_popcountll(peers & lt_mask);
-                    if (sorted_rows) sorted_rows[slot] = static_cast<IdxT>(r);
+                    if (sorted_rows) sorted_rows[slot] = static_cast<IdxT>(R.row_div ? r / R.row_div : r);
                     if (inv) inv[r] = static_cast<IdxT>(slot);
                     if (__builtin_ctzll(peers) == lane) mycnt[key] = before + __builtin_popcountll(peers);
                 } else if (key == E) {
@@ -592,7 +597,7 @@ template <typename IdxT, int HD>
 int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t block_m,
                  IdxT* sorted_rows, int64_t cap, IdxT* expert_ids, int64_t max_blocks, IdxT* inv,
                  int32_t* offsets, const void* hidden, int64_t hstride, int64_t H, f16* a16,
-                 hipStream_t st, int32_t* zero = nullptr, int nzero = 0) {
+                 hipStream_t st, int32_t* zero = nullptr, int nzero = 0, bool token_rows = false) {
     const int64_t Nexp = T * topk;
     unsigned grid = 1;
     if (a16) {
@@ -604,6 +609,10 @@ int launch_route(const int64_t* ids, int64_t T, int64_t topk, int64_t E, int64_t
     }
     const size_t lds_bytes = route_lds_bytes(E);
     RouteOut R{Nexp, cap, max_blocks, block_m, static_cast<int>(E), zero, nzero};
+    if (token_rows) {
+        R.row_div = topk;
+        R.pad_tok = T;
+    }
     hipLaunchKernelGGL((route_kernel<IdxT, HD>), dim3(grid), dim3(kRouteThreads), lds_bytes, st, ids, R,
                        sorted_rows, expert_ids, inv, offsets, hidden, hstride, T, H, a16);
     KSL_LAUNCH_CHECK();
@@ -626,6 +635,32 @@ extern "C" int ksl_moe_align(const int64_t* topk_ids, int64_t T, int64_t topk, i
     return launch_route<int64_t, KSL_DTYPE_BF16>(topk_ids, T, topk, E, block_m, sorted_rows, cap,
                                                  expert_ids, max_blocks, inv, nullptr, nullptr, 0, 0,
                                                  nullptr, static_cast<hipStream_t>(stream));
+}
+
+// Capacity of the moe_align_cuda contract (kernels/fused_moe_w4_v2.py:59-64):
+// mx = Nexp + E*(block_m - 1) slots (at most Nexp*block_m when Nexp < E),
+// rounded up to whole blocks. The used blocks never exceed it: an expert with
+// c > 0 rows takes at most c + block_m - 1 slots.
+extern "C" int64_t ksl_moe_align_i32_capacity(int64_t T, int64_t topk, int64_t E, int64_t block_m) {
+    if (T < 0 || topk <= 0 || E <= 0 || block_m <= 0) return -1;
+    const int64_t Nexp = T * topk;
+    int64_t mx = Nexp + E * (block_m - 1);
+    if (Nexp < E && Nexp * block_m < mx) mx = Nexp * block_m;
+    return (mx + block_m - 1) / block_m * block_m;
+}
+
+extern "C" int ksl_moe_align_i32(const int64_t* topk_ids, int64_t T, int64_t topk, int64_t E,
+                                 int64_t block_m, int32_t* a_row, int32_t* expert_ids, int32_t* inv,
+                                 void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || E <= 0 || E > kMaxExperts || block_m <= 0) return KSL_ERR_SHAPE;
+    if (T * topk >= (int64_t(1) << 31) || T * topk + E * block_m >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    const int64_t cap = ksl_moe_align_i32_capacity(T, topk, E, block_m);
+    if (cap == 0) return KSL_OK;  // no rows: nothing to write
+    if (!topk_ids || !a_row || !expert_ids || !inv) return KSL_ERR_ARG;
+    return launch_route<int32_t, KSL_DTYPE_BF16>(topk_ids, T, topk, E, block_m, a_row, cap, expert_ids,
+                                                 cap / block_m, inv, nullptr, nullptr, 0, 0, nullptr,
+                                                 static_cast<hipStream_t>(stream), nullptr, 0, true);
 }
 
 namespace ksl {

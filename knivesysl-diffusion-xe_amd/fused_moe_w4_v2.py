@@ -31,6 +31,8 @@ Differences from the reference, on purpose:
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -46,6 +48,40 @@ def hidden_device(exp):
         if t is not None:
             return t.device
     return "cpu"
+
+
+@torch.no_grad()
+def moe_align_cuda(topk_ids: torch.Tensor, block_m: int, E: int):
+    """kernels/fused_moe_w4_v2.py:46-76: (a_row int32[cap], expert_ids
+    int32[cap // block_m], cap, inv int32[T*topk]) in one launch
+    (ksl_moe_align_i32). cap follows the reference's capacity rule, padding
+    slots hold T and padding blocks E. Every id must be a real expert in
+    [0, E), as the reference requires; MOE_VALIDATE=1 adds the reference's
+    synchronous range assert (:54-56)."""
+    if topk_ids.dim() != 2:
+        raise ValueError("topk_ids must be [T, topk]")
+    if os.environ.get("MOE_VALIDATE") == "1":
+        mn, mxv = int(topk_ids.min()), int(topk_ids.max())
+        assert 0 <= mn and mxv < E, f"moe_align_cuda: ids must be in [0,{E}); got [{mn},{mxv}]"
+    T, tk = topk_ids.shape
+    block_m, E = int(block_m), int(E)
+    if block_m <= 0 or E <= 0:
+        raise ValueError("block_m and E must be positive")
+    if E > 512:
+        raise ValueError("E > 512 experts is not supported")
+    if not topk_ids.is_cuda:
+        raise ValueError("topk_ids must be on the GPU")
+    lib = _lib.load()
+    cap = int(lib.ksl_moe_align_i32_capacity(T, tk, E, block_m))
+    dev = topk_ids.device
+    ids = topk_ids.to(torch.int64).contiguous()
+    a_row = torch.empty(cap, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(cap // block_m, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * tk, dtype=torch.int32, device=dev)
+    rc = lib.ksl_moe_align_i32(_lib.ptr(ids), T, tk, E, block_m, _lib.ptr(a_row), _lib.ptr(expert_ids),
+                               _lib.ptr(inv), _lib.stream_of(ids))
+    _lib.check(rc, "ksl_moe_align_i32")
+    return a_row, expert_ids, cap, inv
 
 
 def _act_code(fn) -> int | None:

@@ -284,6 +284,37 @@ def moe_align(topk_ids: np.ndarray, block_m: int, E: int):
     return sorted_rows, expert_ids, int(cap), inv
 
 
+def moe_align_cuda(topk_ids: np.ndarray, block_m: int, E: int):
+    """Returns (a_row int32[cap], expert_ids int32[nblk], cap, inv int32[Nexp]).
+
+    The contract of moe_align_cuda (kernels/fused_moe_w4_v2.py:46-76): the same
+    expert-ordered, block_m-aligned layout as moe_align, at the capacity
+    mx = Nexp + E*(block_m - 1) (min(Nexp*block_m, mx) when Nexp < E, :60-62),
+    nblk = ceil(mx / block_m) blocks, cap = nblk * block_m (:63-64); padding
+    blocks carry expert id E (:41-43, marlin's -1 folded to E), and
+    _align_finalize (:32-43) turns the sorted rows into a_row = row // topk for
+    a real row and T for a padding slot, with inv[row] = its sorted position.
+    Rows keep their stable order within an expert (the torch align's order).
+    """
+    topk_ids = np.asarray(topk_ids, dtype=np.int64)
+    T, tk = topk_ids.shape
+    Nexp = T * tk
+    mx = Nexp + E * (block_m - 1)
+    if Nexp < E:
+        mx = min(Nexp * block_m, mx)
+    nblk = (mx + block_m - 1) // block_m
+    cap = nblk * block_m
+    sr, eids, _, inv = moe_align(topk_ids, block_m, E)
+    used_blocks = int((eids < E).sum())
+    used = used_blocks * block_m
+    a_row = np.full(cap, T, dtype=np.int32)
+    s = sr[:used]
+    a_row[:used] = np.where(s < Nexp, s // tk, T)
+    expert_ids = np.full(nblk, E, dtype=np.int32)
+    expert_ids[:used_blocks] = eids[:used_blocks]
+    return a_row, expert_ids, int(cap), inv.astype(np.int32)
+
+
 # ----------------------------------------------------------------------------
 # Activations — kernels/fused_moe_w4_v2.py:136-138 (tanh-GELU), SiLU
 # ----------------------------------------------------------------------------
@@ -360,6 +391,55 @@ def combine_muladd(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.
         rows = out3[inv.reshape(T, tk)[:, k]].astype(np.float32)
         acc = (acc + (w32[:, k:k + 1] * rows).astype(np.float32)).astype(np.float32)
     return acc
+
+
+# ----------------------------------------------------------------------------
+# v1 path — kernels/fused_moe_w4.py:54-128 (_grouped_w4 on gate/up, act_fn in
+# torch, _grouped_w4 on down, combine in fp16 products)
+# ----------------------------------------------------------------------------
+def gateup_raw(a16: np.ndarray, gu_w16: np.ndarray) -> np.ndarray:
+    """out1 = fp16(A @ W^T) over all 2I gate/up rows (fused_moe_w4.py:87-90
+    as :117-118 runs it): fp16 [M, 2I], gate in columns 0..I-1, up in I..2I-1."""
+    return _mm_f32(a16, gu_w16).astype(np.float16)
+
+
+def combine_v1(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.ndarray:
+    """fused_moe_w4.py:125-127: (out3[inv].view(T, tk, H) * w.to(fp16)).sum(1):
+    each product fp16(fp16(w) * x) (torch's fp16 multiply: the exact product,
+    both factors having 11-bit mantissas, rounded once), the tk products summed
+    in fp32 in slot order, the sum rounded to fp16. Returns fp16 [T, H] (the
+    caller casts to hidden.dtype, :127)."""
+    T, tk = topk_w.shape
+    w16 = topk_w.astype(np.float32).astype(np.float16).astype(np.float32)
+    acc = np.zeros((T, out3.shape[1]), dtype=np.float32)
+    for k in range(tk):
+        rows = out3[inv.reshape(T, tk)[:, k]].astype(np.float32)
+        acc = acc + (w16[:, k:k + 1] * rows).astype(np.float16).astype(np.float32)
+    return acc.astype(np.float16)
+
+
+def moe_forward_v1(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
+                   topk_ids: np.ndarray, topk_w: np.ndarray, act16):
+    """One fused_moe_w4 call (fused_moe_w4.py:104-128) with the activation
+    act16 (fp16 array -> fp16 array, the module's act_fn): out2 =
+    fp16(act16(gate) * up) (:119). Returns the fp16 combine [T, H]. Organised
+    per expert; every id must be a real expert."""
+    T, H = hidden_f32.shape
+    E, twoI, _ = gu_q.shape
+    I = twoI // 2
+    tk = topk_ids.shape[1]
+    flat = np.asarray(topk_ids, dtype=np.int64).reshape(-1)
+    a16 = hidden_f32.astype(np.float16)
+    out3_rows = np.zeros((T * tk, H), dtype=np.float16)
+    for e in range(E):
+        r = np.nonzero(flat == e)[0]
+        if r.size == 0:
+            continue
+        out1 = gateup_raw(a16[r // tk], dequant_w4(gu_q[e], gu_s[e], gu_z[e], GU_GS))
+        gate, up = out1[:, :I], out1[:, I:]
+        o2 = (np.asarray(act16(gate), dtype=np.float16).astype(np.float32) * up.astype(np.float32)).astype(np.float16)
+        out3_rows[r] = down(o2, dequant_w4(dn_q[e], dn_s[e], dn_z[e], DN_GS))
+    return combine_v1(out3_rows, np.arange(T * tk), topk_w)
 
 
 def moe_forward(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,

@@ -50,6 +50,8 @@ BARS = {                             # observed on the MI355X (max, mean):
     "prefill_8192": (3.5e-3, 2.0e-5),   # 1.7e-3, 9.6e-6 (192 sampled tokens)
     "layer_fixture": (4.2e-3, 3.2e-3),  # 2.1e-3, 1.6e-3
     "ffn_dropin": (6.0e-3, 3.2e-3),     # 2.8e-3, 1.5e-3
+    "gateup_raw": (1.5e-3, 4.0e-4),     # 7.6e-4, 2.0e-4 (gate and up without activation, v1 path)
+    "forward_v1": (8.0e-3, 1.4e-3),     # 3.9e-3, 6.9e-4 (v1 forward, act_fn in torch)
 }
 
 # (check, test id, normalised max, normalised mean) of every check_norm_err call

@@ -9,6 +9,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 from tests.conftest import ROOT, load_mod
@@ -57,6 +58,17 @@ def test_host_only_calls(L):
     # sorted rows, offsets, inv, a16, out2, out3 at least
     assert a >= 256 * 8 * (704 + 2816) * 2 + 256 * 2816 * 2
     assert b > a
+
+
+def test_align_i32_capacity(L):
+    """The moe_align_cuda capacity rule (kernels/fused_moe_w4_v2.py:59-64) against
+    the oracle's, over block sizes and the rows < experts branch."""
+    from oracle import moe_oracle as mo
+    for T, tk, E, bm in ((256, 8, 128, 32), (256, 8, 128, 16), (3, 2, 64, 16), (1, 1, 512, 64),
+                         (100, 8, 128, 1), (0, 8, 128, 32), (7, 3, 8, 5)):
+        ids = np.zeros((T, tk), dtype=np.int64)
+        assert L.ksl_moe_align_i32_capacity(T, tk, E, bm) == mo.moe_align_cuda(ids, bm, E)[2]
+    assert L.ksl_moe_align_i32_capacity(4, 2, 0, 32) == -1
 
 
 def test_route_scratch_bytes(L):

@@ -159,6 +159,47 @@ def test_moe_align_brute_force_and_c(T, tk, E, bm, seed):
         assert np.array_equal(a, b)
 
 
+def test_moe_align_cuda_known_answer():
+    """The marlin-capacity align of moe_align_cuda by hand: ids [[1,0],[0,2]],
+    block 2, E 3: Nexp 4, mx = 4 + 3*1 = 7, 4 blocks, cap 8; expert 0 holds
+    rows 1, 2 (tokens 0, 1), expert 1 row 0 (token 0) and a pad, expert 2 row
+    3 (token 1) and a pad."""
+    a_row, eids, cap, inv = mo.moe_align_cuda(np.array([[1, 0], [0, 2]]), 2, 3)
+    assert cap == 8
+    assert a_row.tolist() == [0, 1, 0, 2, 1, 2, 2, 2]
+    assert eids.tolist() == [0, 1, 2, 3]
+    assert inv.tolist() == [2, 0, 1, 4]
+    # fewer rows than experts: mx = min(Nexp * block, Nexp + E * (block - 1))
+    a_row, eids, cap, inv = mo.moe_align_cuda(np.array([[5, 1]]), 4, 8)
+    assert cap == 8 and eids.tolist() == [1, 5]
+    assert a_row.tolist() == [0, 1, 1, 1, 0, 1, 1, 1] and inv.tolist() == [4, 0]
+
+
+@pytest.mark.parametrize("T,tk,E,bm,seed", [(37, 8, 16, 4, 1), (3, 2, 64, 16, 2), (100, 8, 128, 1, 3),
+                                          (512, 8, 128, 64, 4)])
+def test_moe_align_cuda_invariants(T, tk, E, bm, seed):
+    """Every routed row sits once in its expert's blocks: a_row[inv[r]] is r's
+    token, the block of inv[r] carries r's expert, slots past the used blocks are
+    padding (T, expert E), and the capacity follows the stated rule."""
+    g = np.random.default_rng(seed)
+    ids = g.integers(0, E, size=(T, tk))
+    a_row, eids, cap, inv = mo.moe_align_cuda(ids, bm, E)
+    N = T * tk
+    mx = N + E * (bm - 1)
+    if N < E:
+        mx = min(N * bm, mx)
+    assert cap == -(-mx // bm) * bm and eids.size == cap // bm and a_row.size == cap
+    flat = ids.reshape(-1)
+    assert len(set(inv.tolist())) == N
+    assert np.array_equal(a_row[inv], np.arange(N) // tk)
+    assert np.array_equal(eids[inv // bm], flat)
+    used = int((eids < E).sum()) * bm
+    assert used == bm * int(sum(-(-int(c) // bm) for c in np.bincount(flat, minlength=E)))
+    assert (a_row[used:] == T).all() and (eids[used // bm:] == E).all()
+    pads = np.setdiff1d(np.arange(used), inv)
+    assert (a_row[pads] == T).all()
+
+
 # --------------------------------------------------------------- activations
 @pytest.mark.parametrize("act", [mo.ACT_GELU_TANH, mo.ACT_SILU])
 def test_activation_closed_forms(act):
@@ -535,3 +576,59 @@ def test_combine_fma_assumption_at_layer_256():
     assert 0.3 < frac32 < 0.7
     assert 0 < n_bf16 < T * H // 1000 and n_bf16 < n_f16
     assert np.abs(y_fma - y_ma).max() <= 2 * np.spacing(np.abs(y_fma).max())
+
+
+# ---------------------------------------------------------------- v1 path
+def test_combine_v1_known_answer_and_torch():
+    """The v1 combine (kernels/fused_moe_w4.py:125-127). Known answer: w = 0.1
+    is fp16 0.0999755859375, times 3 is 0.2999267578125, exactly halfway
+    between the fp16 neighbours 1228 and 1229 * 2^-12: round-half-even gives
+    0.2998046875 (an fp32 product would keep 0.29992676). Then the reference's
+    own expression evaluated by torch on the CPU in fp16 agrees bit for bit
+    on random data, and the fp32-chain combine does not (the fp16 roundings
+    show)."""
+    y = mo.combine_v1(np.array([[3.0]], np.float16), np.array([0]), np.array([[0.1]], np.float32))
+    assert y.dtype == np.float16 and float(y[0, 0]) == 0.2998046875
+    # two slots: products 0.2998046875 and fp16(0.5 * 2^-11) = 2^-12, fp32 sum, fp16 round
+    y2 = mo.combine_v1(np.array([[3.0], [2.0 ** -11]], np.float16), np.array([0, 1]),
+                       np.array([[0.1, 0.5]], np.float32))
+    assert float(y2[0, 0]) == float(np.float16(0.2998046875 + 2.0 ** -12))
+    g = np.random.default_rng(31)
+    T, tk, H = 64, 8, 256
+    out3 = (0.3 * g.standard_normal((T * tk, H))).astype(np.float16)
+    inv = g.permutation(T * tk)
+    w = g.dirichlet(np.ones(tk), size=T).astype(np.float32)
+    ref = (torch.from_numpy(out3)[torch.from_numpy(inv)].view(T, tk, H)
+           * torch.from_numpy(w).to(torch.float16).unsqueeze(-1)).sum(dim=1)
+    got = mo.combine_v1(out3, inv, w)
+    assert np.array_equal(got.view(np.uint16), ref.numpy().view(np.uint16))
+    fma = mo.combine_fma(out3, inv, w).astype(np.float16)
+    assert not np.array_equal(got, fma)
+
+
+def test_moe_forward_v1_matches_v2_for_the_same_activation():
+    """With act_fn = tanh-GELU the v1 forward differs from v2 only by where
+    the activation is rounded (fp16 gate, fp16 act output, fp16 combine
+    products): the two agree to a few fp16 ulps, and v1's out1 is the gate/up
+    GEMM the v2 oracle evaluates (gateup_act from the same gate and up)."""
+    g = np.random.default_rng(32)
+    E, H, I, T, tk = 4, 256, 128, 12, 2
+    gu_q, gu_s, gu_z = mo.quantize_w4(g.standard_normal((E * 2 * I, H)).astype(np.float32), mo.GU_GS)
+    dn_q, dn_s, dn_z = mo.quantize_w4((0.1 * g.standard_normal((E * H, I))).astype(np.float32), mo.DN_GS)
+    gu = [a.reshape(E, 2 * I, -1) for a in (gu_q, gu_s, gu_z)]
+    dn = [a.reshape(E, H, -1) for a in (dn_q, dn_s, dn_z)]
+    hid = (0.05 * g.standard_normal((T, H))).astype(np.float32)
+    ids = np.stack([g.permutation(E)[:tk] for _ in range(T)])
+    w = g.dirichlet(np.ones(tk), size=T).astype(np.float32)
+
+    def gelu16(x):
+        return torch.nn.functional.gelu(torch.from_numpy(x).float(), approximate="tanh").half().numpy()
+
+    y1 = mo.moe_forward_v1(hid, *gu, *dn, ids, w, gelu16).astype(np.float32)
+    y2 = mo.moe_forward_per_expert(hid, *gu, *dn, ids, w, mo.ACT_GELU_TANH)[0]
+    assert np.abs(y1 - y2).max() <= 4e-3 * np.abs(y2).max()
+    a16 = hid.astype(np.float16)[:3]
+    w16 = mo.dequant_w4(gu[0][0], gu[1][0], gu[2][0], mo.GU_GS)
+    o1 = mo.gateup_raw(a16, w16)
+    assert np.array_equal(o1[:, :I], mo._mm_f32(a16, w16[:I]).astype(np.float16))
+    assert np.array_equal(o1[:, I:], mo._mm_f32(a16, w16[I:]).astype(np.float16))

@@ -73,6 +73,43 @@ def test_moe_align_empty(gpu):
     assert inv.numel() == 0
 
 
+ALIGN_I32_CASES = [
+    # (T, topk, E, block_m, seed, zipf): marlin capacity, fewer rows than experts,
+    # block 1, a heavy Zipf routing, 512 experts
+    (256, 8, 128, 32, 21, None),
+    (256, 8, 128, 16, 22, None),
+    (3, 2, 64, 16, 23, None),
+    (100, 8, 128, 1, 24, None),
+    (8192, 8, 128, 32, 25, 1.1),
+    (300, 2, 512, 8, 26, None),
+]
+
+
+@pytest.mark.parametrize("T,tk,E,bm,seed,zipf", ALIGN_I32_CASES)
+def test_moe_align_cuda_bit_exact(gpu, T, tk, E, bm, seed, zipf):
+    """The int32 token-row align (moe_align_cuda, kernels/fused_moe_w4_v2.py:46-76)
+    against the oracle, every output bit-exact, every id a real expert."""
+    v2 = load_mod("fused_moe_w4_v2")
+    wl = load_mod("workloads")
+    ids, _ = wl.make_routing(T, E, tk, seed, zipf)
+    ref = mo.moe_align_cuda(ids.numpy(), bm, E)
+    got = v2.moe_align_cuda(ids.to(gpu), bm, E)
+    assert got[2] == ref[2]
+    for name, g, r in (("a_row", got[0], ref[0]), ("expert_ids", got[1], ref[1]), ("inv", got[3], ref[3])):
+        assert g.dtype == torch.int32, name
+        assert np.array_equal(_np(g), r), name
+
+
+def test_moe_align_cuda_empty_and_int32_ids(gpu):
+    v2 = load_mod("fused_moe_w4_v2")
+    a_row, eids, cap, inv = v2.moe_align_cuda(torch.empty(0, 8, dtype=torch.int64, device=gpu), 32, 128)
+    assert cap == 0 and a_row.numel() == 0 and eids.numel() == 0 and inv.numel() == 0
+    ids = torch.tensor([[1, 0], [0, 2]], dtype=torch.int32, device=gpu)  # converted to int64 by the wrapper
+    a_row, eids, cap, inv = v2.moe_align_cuda(ids, 2, 3)
+    assert cap == 8 and _np(a_row).tolist() == [0, 1, 0, 2, 1, 2, 2, 2]
+    assert _np(eids).tolist() == [0, 1, 2, 3] and _np(inv).tolist() == [2, 0, 1, 4]
+
+
 def _route(gpu, ids, hidden, E):
     """ksl_moe_route through the C ABI. Returns (sorted_rows, offsets, inv, a16)."""
     lib = load_pkg()._lib
