@@ -1,7 +1,8 @@
 // Expert GEMMs of large routings (prefill: more than 8192 routed rows) for
 // gfx950, in GEMM form: one workgroup per (block of up to 128 rows of one
-// expert, block of output columns), eight waves, each wave owning all 128
-// rows x 64 weight rows of the block (8 x 4 tiles of v_mfma_f32_16x16x32_f16).
+// expert, block of 256 weight rows), four waves, each wave owning all 128
+// rows x 64 weight rows of the block (8 x 4 tiles of v_mfma_f32_16x16x32_f16),
+// two workgroups per CU.
 //
 // Why this shape: with a 16-column tile per wave every MFMA needs its own
 // 1 KB activation fragment from LDS, and at prefill the LDS read port, not
@@ -11,13 +12,15 @@
 // the nibble decode over 32 MFMAs.
 //
 // Pipeline: per 128-K quantisation group (one slot) the workgroup needs the
-// block's activation fragments (8 M tiles x 4 steps x 1 KB) and its weight
-// fragments (8 waves x 4 tiles x 1 KB); both go into a two-slot LDS ring by
-// direct global -> LDS loads. Every wave issues its share of the next group
-// (its own weight tiles, and the activation tile whose index is its wave
-// number) before computing the current one, then waits for its own loads
-// and joins one workgroup barrier per group. The scales and zero-points of
-// the block's 512 weight rows sit in LDS for the whole K loop (fp16 scales,
+// block's activation fragments (8 M tiles x 4 steps x 1 KB), which go into a
+// two-slot LDS ring by direct global -> LDS loads, and each wave its own
+// weight fragments (4 tiles x 1 KB), loaded straight into registers. Every
+// wave issues its share of the next group (its weight tiles, and the
+// activation tiles whose index is its wave number) before computing the
+// current one, then waits for its own loads and joins one workgroup barrier
+// per group; the loads of group g + 1 are in flight while group g's MFMAs run
+// (see `stage`). The scales and zero-points of
+// the block's 256 weight rows sit in LDS for the whole K loop (fp16 scales,
 // zero-points as nibbles, so that the table fits beside the ring).
 //
 // Numerics: B = fp16((q - z) * s) per weight as the reference dequantises
@@ -175,8 +178,7 @@ __global__ __launch_bounds__(kRbThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             arow[h] = reinterpret_cast<const char*>(A.act) + (row * K + ch * 8) * 2;
         }
     }
-    auto issue_act = [&](int g, int slot) {
-        char* base = lds + slot * kRbSlot;
+    auto issue_act_p = [&](int g, char* base) {
         const int nst = has_tail && g == G2 ? 2 : 4;  // the 64-K tail group has two steps
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -186,6 +188,7 @@ __global__ __launch_bounds__(kRbThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             }
         }
     };
+    auto issue_act = [&](int g, int slot) { issue_act_p(g, lds + slot * kRbSlot); };
     // weights: this lane's 16 bytes of each of its 4 tiles for one 128-K
     // group, straight into registers (lane (col, c): row col, K 32c .. +32);
     // the tail group's 8 bytes (K 16c .. +16)
@@ -227,10 +230,9 @@ __global__ __launch_bounds__(kRbThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
             for (int n = 0; n < kRbNt; ++n) acc[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
         // one slot's MFMAs; wv[n][i]: tile n's weight word of step i
-        auto compute = [&](int g, const auto& wv, auto nstep_c) {
+        auto compute_p = [&](int g, const char* sp, const auto& wv, auto nstep_c) {
             constexpr int NSTEP = decltype(nstep_c)::value;
             const bool tail = NSTEP == 2;
-            const char* sp = lds + (g & 1) * kRbSlot;
             // this lane's scale group in slot g
             const int gs = KIND == kRbGateUp ? g : (tail ? 2 * G2 : 2 * g + (c >> 1));
             f16x2 sc[kRbNt];
@@ -267,28 +269,40 @@ __global__ __launch_bounds__(kRbThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                 }
             }
         };
+        auto compute = [&](int g, const auto& wv, auto nstep_c) { compute_p(g, lds + (g & 1) * kRbSlot, wv, nstep_c); };
+        // One group of the K loop: the next slot's direct-to-LDS loads, the
+        // next group's weights, this slot's MFMAs. The compiler makes an LDS
+        // read wait (vmcnt) for every outstanding direct-to-LDS load it cannot
+        // tell apart from it; issued and read through two restrict pointers of
+        // one inlined call, they carry disjoint alias scopes and the reads of
+        // slot g run while slot g + 1 and the weights of group g + 1 are in
+        // flight. (With the slot pointers computed in place, the generated
+        // code waited for all of them before the first read: load and compute
+        // ran one after the other.)
+        auto stage = [&](int g, char* __restrict__ dst, const char* __restrict__ src, auto& wc_, auto& wn_) {
+            if (g + 1 < NS) issue_act_p(g + 1, dst);
+            if (active) {
+                if (g + 1 < G2) load_w(g + 1, wn_);
+                compute_p(g, src, wc_, std::integral_constant<int, 4>{});
+            }
+        };
         // weights one group ahead in registers, activations one group ahead
         // in the LDS ring; each wave waits for its own loads, then one
         // barrier per group publishes the slot and frees the other one
         u32x4 wc[kRbNt], wn[kRbNt] = {};
         u32x2 wt[kRbNt];
         issue_act(0, 0);
-        if (G2 > 0) {
-            if (active) load_w(0, wc);
-        } else if (active) {
-            load_w_tail(wt);
+        // the tail group's weights with the first group's, held in registers
+        // through the loop: a load of them inside the loop made the compiler
+        // copy (and so wait for) the buffer on every trip
+        if (active) {
+            if (G2 > 0) load_w(0, wc);
+            if (has_tail) load_w_tail(wt);
         }
         vm_wait<0>();
         __syncthreads();  // group 0 and the table are in LDS
         for (int g = 0; g < G2; ++g) {
-            if (g + 1 < NS) issue_act(g + 1, (g + 1) & 1);
-            if (active) {
-                if (g + 1 < G2)
-                    load_w(g + 1, wn);
-                else if (has_tail)
-                    load_w_tail(wt);
-                compute(g, wc, std::integral_constant<int, 4>{});
-            }
+            stage(g, lds + ((g + 1) & 1) * kRbSlot, lds + (g & 1) * kRbSlot, wc, wn);
             vm_wait<0>();     // this wave's loads of group g + 1 have landed
             __syncthreads();  // everyone's have, and slot g is free
 #pragma unroll
