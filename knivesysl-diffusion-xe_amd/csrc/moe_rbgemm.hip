@@ -250,9 +250,43 @@ __global__ __launch_bounds__(kRbThreads) __attribute__((amdgpu_waves_per_eu(2, 2
                     f16x8 b[kRbNt];
 #pragma unroll
                     for (int n = 0; n < kRbNt; ++n) b[n] = nib8_dequant(wv[n][i], zc[n], sc[n], kn);
+                    if constexpr (FULL) {
+                        // Activation fragments read one M tile ahead of their
+                        // MFMAs, by asm: with the accumulators, the weights and
+                        // the decoded fragments in registers the compiler keeps
+                        // one fragment register and waits for each read right
+                        // before its MFMAs. Each read's destination is left
+                        // untouched until the wait before its use (checked on
+                        // the generated code by tests/test_cpu_codegen.py).
+                        const uint32_t ap = static_cast<uint32_t>(
+                            reinterpret_cast<uintptr_t>((lds_vptr)const_cast<char*>(sp + i * kBlk + fo)));
+                        f16x8 a;
+                        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(a) : "v"(ap) : "memory");
+#pragma unroll
+                        for (int t = 0; t < kRbMt; ++t) {
+                            f16x8 an;
+                            if (t + 1 < kRbMt)
+                                asm volatile("ds_read_b128 %0, %1 offset:%2 ; ksl-ahead"
+                                             : "=v"(an)
+                                             : "v"(ap), "i"((t + 1) * 4 * kBlk)
+                                             : "memory");
+#pragma unroll
+                            for (int n = 0; n < kRbNt; ++n) {
+                                if constexpr (KIND == kRbGateUp)
+                                    acc[t][n] = mfma16x16x32(a, b[n], acc[t][n]);
+                                else
+                                    acc[t][n] = mfma16x16x32(b[n], a, acc[t][n]);
+                            }
+                            if (t + 1 < kRbMt) {
+                                __builtin_amdgcn_sched_barrier(0);
+                                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(an) : : "memory");
+                                a = an;
+                            }
+                        }
+                    } else
 #pragma unroll
                     for (int t = 0; t < kRbMt; ++t) {
-                        if (FULL || t < mt) {
+                        if (t < mt) {
                             const f16x8 a = *reinterpret_cast<const f16x8*>(sp + (t * 4 + i) * kBlk + fo);
 #pragma unroll
                             for (int n = 0; n < kRbNt; ++n) {

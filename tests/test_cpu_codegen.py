@@ -11,8 +11,9 @@ may come from a register whose load had not landed. Shapes: the 256-token
 layer (one chunk, up to two M tiles), 1024 tokens (four M tiles, several
 chunks per expert), a Zipf routing of 1024 tokens (experts of a few to many
 chunks), and small / odd I (a 64-K tail group, the largest I). Above 8192
-routed rows a different kernel runs (moe_rbgemm.hip), whose weights go
-through LDS by direct loads and ordinary register loads only."""
+routed rows a different kernel runs (moe_rbgemm.hip): ordinary register
+loads for its weights, and inline-asm LDS reads of its activation fragments,
+whose in-flight windows are checked below on the generated code."""
 from __future__ import annotations
 
 import importlib.util
@@ -167,3 +168,92 @@ def test_down_kernel_every_width(down_asm, layout):
     for G in range(1, 17):
         I = 64 * G
         test_down_kernel_addresses_and_register_flow(down_asm, 4, 128, I, 48, 2, "uniform", layout, (0, 5))
+
+
+# ---- the row-block GEMMs (moe_rbgemm.hip): activation fragments read by asm
+@pytest.fixture(scope="module")
+def rb_asm(tmp_path_factory):
+    hipcc, flags = _build_flags()
+    if not (os.path.exists(hipcc) or shutil.which(hipcc)):
+        pytest.skip("hipcc not available")
+    out = str(tmp_path_factory.mktemp("asm") / "moe_rbgemm.s")
+    res = subprocess.run([hipcc, *flags, "-w", "--cuda-device-only", "-S", os.path.join(CSRC, "moe_rbgemm.hip"),
+                          "-o", out], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-4000:]
+    return out
+
+
+def _vregs(tok):
+    import re
+    m = re.match(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def _ahead_windows(lines):
+    """For every `ds_read_b128 ...; ksl-ahead` (an LDS read issued by inline asm
+    whose result the compiler believes present at once), the instructions up to
+    the next s_waitcnt that retires it. Returns (reads, violations): a
+    violation is an instruction in the window that reads or writes one of the
+    destination registers, or a branch or label inside the window."""
+    reads, bad = 0, []
+    for i, line in enumerate(lines):
+        if "ksl-ahead" not in line or "ds_read_b128" not in line:
+            continue
+        reads += 1
+        dst = _vregs(line.split()[1].rstrip(","))
+        assert len(dst) == 4, line
+        for j in range(i + 1, len(lines)):
+            s = lines[j].split(";")[0].strip()
+            if not s:
+                continue
+            if s.startswith("s_waitcnt") and "lgkmcnt(0)" in s:
+                break
+            if s.endswith(":") or s.startswith("s_cbranch") or s.startswith("s_branch") or s.startswith("s_setpc"):
+                bad.append((i, s))
+                break
+            used = set()
+            for t in s.split()[1:]:
+                used |= _vregs(t.strip(","))
+            if used & dst:
+                bad.append((i, s))
+        else:
+            bad.append((i, "no wait before the function ends"))
+    return reads, bad
+
+
+def test_rb_gemm_ahead_reads_stay_untouched_in_flight(rb_asm):
+    """Every row-block kernel instance (gate/up and down, both activations and
+    both weight layouts): each asm LDS read of the next M tile's activation
+    fragment keeps its four destination registers untouched, with no branch,
+    until the s_waitcnt lgkmcnt(0) that retires it; seven such reads per
+    128-K step of the full-block path."""
+    text = open(rb_asm).read().split("\n")
+    fns = [l.split(":")[0] for l in text if l.startswith("_ZN3ksl12_GLOBAL__N_114rb_gemm_kernel")
+           and l.split(";")[0].strip().endswith(":")]
+    assert len(fns) == 4
+    for fn in fns:
+        i0 = next(i for i, l in enumerate(text) if l.startswith(fn + ":"))
+        ins = []
+        for l in text[i0 + 1:]:
+            if l.startswith(".Lfunc_end"):
+                break
+            ins.append(l.strip())
+        reads, bad = _ahead_windows(ins)
+        # gate/up: 4 steps of 7; down: 4 + 2 (the 64-K tail) steps of 7
+        assert reads in (28, 42), (fn, reads)
+        assert not bad, (fn, bad[:5])
+
+
+def test_ahead_window_check_flags_a_touched_register():
+    """The window check itself: a planted use of an in-flight destination, and
+    a branch inside a window, are both reported."""
+    ok = ["ds_read_b128 v[4:7], v2 offset:4096 ; ksl-ahead", "v_mfma_f32_16x16x32_f16 v[8:11], v[0:3], v[12:15], v[8:11]",
+          "s_waitcnt lgkmcnt(0)", "v_mov_b32 v4, 0"]
+    assert _ahead_windows(ok) == (1, [])
+    touched = ["ds_read_b128 v[4:7], v2 offset:4096 ; ksl-ahead", "v_mov_b32 v30, v5", "s_waitcnt lgkmcnt(0)"]
+    assert len(_ahead_windows(touched)[1]) == 1
+    branch = ["ds_read_b128 v[4:7], v2 ; ksl-ahead", "s_cbranch_scc1 .LBB0_1", "s_waitcnt lgkmcnt(0)"]
+    assert len(_ahead_windows(branch)[1]) == 1
