@@ -10,6 +10,13 @@ Synthetic seeded data. Inputs are resident in HBM before the timed region.
 A "step" is one layer. Consecutive steps rotate over independent weight sets
 (3 x 412 MB by default) so the 256 MB MALL cannot serve weights from cache.
 
+Settling: a fresh process's first ~20 ms of this workload run up to 20% slower
+than its steady state (the per-step time decays over ~150 steps; 200 ms of
+unrelated matmul or copy work beforehand does not remove it). Before the W
+warmup steps of each timed pass the bench therefore runs the pass's own
+workload for --settle-ms (50 ms by default; 0 turns it off), reported as
+config.settle_ms; the warmup and timed steps are then as given.
+
 Timed passes (all inside this process, on one stream):
   1. value: K steps of the layer (one C call per step: routing + RMSNorm +
      fp16 activations, gate/up, down, combine; with --ffn gate/up and down
@@ -157,6 +164,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--weight-sets", type=int, default=3)
+    ap.add_argument("--settle-ms", type=float, default=50.0,
+                    help="run each timed pass's workload this long before its warmup steps (0: off)")
     ap.add_argument("--act", choices=["silu", "gelu"], default="silu")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -226,7 +235,21 @@ def main() -> int:
         if rc:
             lib.check(rc, "ksl_moe_layer_forward")
 
+    def settle(fn):
+        # the workload itself, until settle_ms of GPU time have passed
+        if args.settle_ms <= 0:
+            return
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + args.settle_ms * 1e-3
+        i = 0
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn(sets[i % len(sets)])
+                i += 1
+            torch.cuda.synchronize()
+
     # ---- pass 1: whole-layer time -------------------------------------------
+    settle(step)
     for i in range(args.warmup):
         step(sets[i % len(sets)])
     torch.cuda.synchronize()
@@ -542,6 +565,7 @@ def main() -> int:
             if rc:
                 lib.check(rc, "ksl_moe_layer_forward")
 
+        settle(pstep)
         for i in range(3):
             pstep(sets[i % len(sets)])
         torch.cuda.synchronize()
@@ -634,6 +658,7 @@ def main() -> int:
                          f"gu gs128 / dn gs64, {args.act}, fixed-order combine -> bf16"),
             "tokens": T, "experts": E, "topk": TOPK, "hidden": H, "intermediate": I,
             "act": args.act, "weight_sets": args.weight_sets, "experts_touched": n_touched,
+            "settle_ms": args.settle_ms,
             "layer_algorithmic_bytes": layer_bytes,
             "layer_GBps": round(layer_gbps, 1),
             "layer_frac_of_hbm_peak": round(layer_gbps / HBM_PEAK_GBPS, 4),
