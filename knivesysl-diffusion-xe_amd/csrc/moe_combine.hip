@@ -584,7 +584,7 @@ extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t t
                            norm_w_dtype, eps, H, a16, bcnt, static_cast<hipStream_t>(stream), nullptr, 0);
 }
 
-extern "C" int ksl_version(void) { return 4; }
+extern "C" int ksl_version(void) { return 5; }
 
 extern "C" const char* ksl_status_string(int status) {
     switch (status) {
