@@ -82,7 +82,9 @@ def fused_moe_w4(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torc
     st = _lib.stream_of(hidden)
     ids = topk_ids.to(torch.int64).contiguous()
     w = topk_w.contiguous()
-    x = hidden if hidden.stride(1) == 1 and hidden.stride(0) % 8 == 0 else hidden.contiguous()
+    aligned = hidden.stride(1) == 1 and hidden.stride(0) % 8 == 0 and hidden.data_ptr() % 16 == 0
+    # a fresh allocation (16-byte aligned) where the routing launch cannot read in place
+    x = hidden if aligned else torch.empty(T, H, dtype=hidden.dtype, device=dev).copy_(hidden)
     sorted_rows = torch.empty(Nexp, dtype=torch.int32, device=dev)
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
     inv = torch.empty(Nexp, dtype=torch.int32, device=dev)

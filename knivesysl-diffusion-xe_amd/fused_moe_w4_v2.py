@@ -292,7 +292,7 @@ def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: t
     dev = hidden.device
     _same_device(dev, topk_ids=topk_ids, topk_w=topk_w, gu_q=exp.gu_q)
     if hidden.stride(1) != 1 or hidden.stride(0) % 8 != 0 or hidden.data_ptr() % 16 != 0:
-        hidden = hidden.contiguous()
+        hidden = hidden.clone(memory_format=torch.contiguous_format)  # a fresh, aligned copy
     ids = topk_ids if topk_ids.dtype == torch.int64 else topk_ids.to(torch.int64)
     ids = ids.contiguous()
     w = topk_w.contiguous()

@@ -36,7 +36,7 @@ def _prepare(exp, x, E, H, I):
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("moe_layer takes bf16 or fp16 activations")
     if x.stride(1) != 1 or x.stride(0) % 8 != 0 or x.data_ptr() % 16 != 0:
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)  # a fresh, aligned copy
     return x
 
 

@@ -28,7 +28,7 @@ from .fused_moe_w4_v2 import _check_act, _check_weights, dn_layout, moe_workspac
 def _rows(t: torch.Tensor, H: int) -> torch.Tensor:
     x = t.reshape(-1, H)
     if x.stride(-1) != 1 or x.stride(0) % 8 != 0 or x.data_ptr() % 16 != 0:
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)  # a fresh, aligned copy
     return x
 
 

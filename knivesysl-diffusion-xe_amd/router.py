@@ -20,7 +20,7 @@ def router_forward(self, hidden_states: torch.Tensor):
     top_k_index int64 [T, k]) as DiffusionGemmaTextRouter.forward returns them."""
     x = hidden_states.reshape(-1, hidden_states.shape[-1])
     if x.stride(-1) != 1 or x.stride(0) % 8 != 0 or x.data_ptr() % 16 != 0:
-        x = x.contiguous()
+        x = x.clone(memory_format=torch.contiguous_format)  # a fresh, aligned copy
     T, H = x.shape
     proj = self.proj.weight
     E = proj.shape[0]

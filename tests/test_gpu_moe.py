@@ -627,3 +627,21 @@ def test_down_at_lds_limited_shapes(gpu, E, H, I):
     ref = np.stack([mo.down(x[i:i + 1], mo.dequant_w4(dn_q[e].numpy(), dn_s[e].numpy(), dn_z[e].numpy(),
                                                           mo.DN_GS))[0] for i, e in enumerate(experts)])
     check_norm_err("down", out3.float().cpu().numpy(), ref.astype(np.float32), f"E={E} H={H} I={I}")
+
+
+def test_forward_accepts_a_misaligned_contiguous_hidden(gpu):
+    """A contiguous hidden starting 2 bytes into its storage (not 16-byte
+    aligned): the drop-in copies it and gives the aligned input's bits."""
+    v2 = load_mod("fused_moe_w4_v2")
+    wl = load_mod("workloads")
+    T, tk, E, H, I = 32, 4, 8, 256, 128
+    exp = wl.make_experts(E, H, I, 95, act="silu").to(gpu)
+    ids, w = wl.make_routing(T, E, tk, 96)
+    hidden = wl.make_hidden(T, H, 97).to(gpu)
+    ref = v2.fused_moe_w4_v2(hidden, exp, ids.to(gpu), w.to(gpu))
+    flat = torch.zeros(T * H + 1, dtype=hidden.dtype, device=gpu)
+    off = flat[1:].view(T, H)
+    off.copy_(hidden)
+    assert off.is_contiguous() and off.data_ptr() % 16 != 0
+    y = v2.fused_moe_w4_v2(off, exp, ids.to(gpu), w.to(gpu))
+    assert torch.equal(ref.view(torch.int16), y.view(torch.int16))

@@ -149,3 +149,25 @@ def test_fused_moe_w4_v1_forward(gpu, T, tk, E, H, I, seed, act):
     check_norm_err("forward_v1", y.float().cpu().numpy(), ref_b, f"{act} T={T} E={E} H={H} I={I}")
     y2 = v1.fused_moe_w4(hidden.to(gpu), expg, ids.to(gpu), w.to(gpu))
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+def test_fused_moe_w4_v1_strided_and_offset_hidden(gpu):
+    """A row-strided view, and a view starting 2 bytes into its storage (not
+    16-byte aligned): the same bits as the contiguous input (the wrapper copies
+    what the routing launch cannot read in place)."""
+    v1 = load_mod("fused_moe_w4")
+    wl = load_mod("workloads")
+    T, tk, E, H, I = 32, 4, 8, 256, 128
+    exp = wl.make_experts(E, H, I, 91).to(gpu)
+    ids, w = wl.make_routing(T, E, tk, 92)
+    hidden = wl.make_hidden(T, H, 93).to(gpu)
+    ref = v1.fused_moe_w4(hidden, exp, ids.to(gpu), w.to(gpu))
+    wide = torch.zeros(T, H + 24, dtype=hidden.dtype, device=gpu)
+    wide[:, :H] = hidden
+    y1 = v1.fused_moe_w4(wide[:, :H], exp, ids.to(gpu), w.to(gpu))
+    flat = torch.zeros(T * H + 1, dtype=hidden.dtype, device=gpu)
+    off = flat[1:].view(T, H)
+    off.copy_(hidden)
+    y2 = v1.fused_moe_w4(off, exp, ids.to(gpu), w.to(gpu))
+    assert torch.equal(ref.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(ref.view(torch.int16), y2.view(torch.int16))
