@@ -256,6 +256,15 @@ size_t ksl_moe_down_lds_bytes(int64_t E, int64_t H, int64_t I, int64_t cus);
 int ksl_quantize_w4(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t group_size, uint8_t* qpacked,
                     void* scale, void* zero, void* stream);
 
+/* dequant_w4 (kernels/w4a16.py:35-48): W [rows, K] fp16 = fp16((q - zero) *
+ * scale), the difference and the product in fp32 as the reference's torch
+ * expression evaluates them (its nibbles promoted against the fp32 scale and
+ * zero), rounded once. qpacked uint8 [rows, K/2] (4-byte aligned), scale and
+ * zero fp16 [rows, K/group_size], out fp16 [rows, K] (16-byte aligned);
+ * group_size % 8 == 0, K % group_size == 0. */
+int ksl_dequant_w4(const uint8_t* qpacked, const void* scale, const void* zero, int64_t rows, int64_t K,
+                   int64_t group_size, void* out, void* stream);
+
 /* The MOE_NS down pack back to the reference layout (load time, out of
  * place): ns_q uint8 [E, I/2, H], the layout the reference's preshuffle_T_dn
  * writes for its _down_nsT_kernel (kernels/fused_moe_w4_v2.py:187-206; in
@@ -266,6 +275,13 @@ int ksl_quantize_w4(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t
  * for the tiled layout. */
 int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q,
                               void* stream);
+
+/* preshuffle_T_dn (kernels/fused_moe_w4_v2.py:186-197), the forward direction
+ * of the above: dn_q uint8 [E, H, I/2] in the reference layout -> ns_q uint8
+ * [E, I/2, H], the MOE_NS pack that enable_ns_down installs (:200-206), byte
+ * for byte. Out of place; H % 64 == 0, I % 64 == 0, 8-byte aligned. */
+int ksl_moe_preshuffle_ns_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* ns_q,
+                               void* stream);
 
 /* Load-time repack of the down weights into the layout the down kernel loads
  * (the reference's precedent is the preshuffled down pack,
@@ -288,14 +304,31 @@ int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, ui
  * counters (one per 256 bytes: the unit queue, an error word, an exit count,
  * one per expert) that must be zero on entry (torch.zeros once); the launch
  * leaves them zero (the last workgroup to finish clears them), except the
- * error word (int32 index 64), which becomes 1 if a wait for another
- * workgroup ran out of its bound (then the output is not to be trusted). Calls that share one ctl
+ * error word (int32 index 64), which becomes 1 if a down unit's wait for its
+ * expert's gate/up units (in other workgroups) ran out of its bound; the unit
+ * then runs anyway, so out2 / out3 of that launch are not to be trusted. Here
+ * the error word latches: only the caller clears it. Inside the fused
+ * forwards (ksl_moe_w4a16_forward, ksl_moe_layer_forward and its no-allocation
+ * variant, ksl_moe_block_forward) the routing launch clears it at the start
+ * of each call and the combine launch of the same call reads it: when it is
+ * set, every element of that call's output y is NaN (the status cannot reach
+ * the caller without a host synchronisation). Calls that share one ctl
  * buffer must not overlap. T*topk <= 8192, E <= 512, H % 128 == 0,
  * I % 64 == 0, H, I <= 8192. */
 size_t ksl_moe_ffn_ctl_bytes(int64_t E);
 int ksl_moe_ffn(const void* a16, const int32_t* sorted_rows, const int32_t* offsets, int64_t T, int64_t topk,
                 const uint8_t* gu_pack, const uint8_t* dn_pack, int64_t E, int64_t H, int64_t I, int act,
                 void* out2, void* out3, int32_t* ctl, void* stream);
+
+/* Bound of the one-launch FFN's dependency wait, for later launches of this
+ * process (no reference counterpart: the reference launches gate/up and down
+ * separately and never waits across workgroups). cycles: empty ring cycles a
+ * down unit waits before it gives up and sets the error word (< 0: the
+ * default, 2^18; at most 2^30). force_wait != 0 makes every dependency count
+ * as unmet, so each down unit waits out the bound and the error word is set
+ * while every workgroup still finishes normally: the host-forced failure of
+ * the failure-handling tests. */
+int ksl_moe_ffn_set_wait_limit(int64_t cycles, int force_wait);
 
 /* Load-time pack of the experts for the one-launch expert FFN (the
  * reference's precedent for a kernel-specific load-time repack is the
@@ -341,6 +374,19 @@ int ksl_moe_combine(const void* out3, const int32_t* inv, const void* topk_w, in
 int ksl_moe_combine_v1(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
                        int64_t T, int64_t topk, int64_t H, void* y, int y_dtype, int64_t y_stride,
                        void* stream);
+
+/* The combine of the stock experts loop that packed_experts_forward runs
+ * (kernels/pack_experts.py:44-62; TF modeling_diffusion_gemma.py:578-588):
+ * y = 0 in y_dtype, then expert by expert in ascending id, each of its rows
+ * adds term = y_dtype(h * w[t,k]) with one rounding to y_dtype per add
+ * (index_add_), h = out3[inv[t*topk+k], :] fp16; h * w is taken in fp32 for
+ * fp32 or bf16 weights and in fp16 for fp16 weights (torch's type
+ * promotion). Per token the slots go in (expert id, slot) order; ids outside
+ * [0, E) are skipped. topk_ids int64 [T, topk] (8-byte aligned), topk <= 32;
+ * other arguments as ksl_moe_combine. */
+int ksl_moe_combine_stock(const void* out3, const int32_t* inv, const int64_t* topk_ids, int64_t E,
+                          const void* topk_w, int w_dtype, int64_t T, int64_t topk, int64_t H, void* y,
+                          int y_dtype, int64_t y_stride, void* stream);
 
 /* Expert router, the step before the MoE: TF modeling_diffusion_gemma.py:529-548
  * (DiffusionGemmaTextRouter.forward), its scale-free norm being the fused

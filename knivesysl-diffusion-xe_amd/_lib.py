@@ -17,8 +17,11 @@ LIB_PATH = os.path.join(PKG_DIR, "libksl.so")
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 ACT_GELU_TANH, ACT_SILU, ACT_NONE = 0, 1, 2
 DN_LAYOUT_REF, DN_LAYOUT_TILED = 0, 1
+ERR_ARG, ERR_SHAPE, ERR_ALIGN = 1, 2, 3
 ERR_SCRATCH, ERR_RUNTIME = 6, 7
 NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
+# int32 index of the one-launch FFN's error word in its ctl counters
+FFN_ERROR_WORD = 64
 
 _TORCH_TO_CODE = {
     torch.float32: DTYPE_F32,
@@ -48,9 +51,12 @@ SIGNATURES = {
     "ksl_quantize_w4": ([_P, _I, _I64, _I64, _I64, _P, _P, _P, _P], _I),
     "ksl_moe_down_lds_bytes": ([_I64, _I64, _I64, _I64], _SZ),
     "ksl_moe_unshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_moe_preshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_dequant_w4": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_combine_v1": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
+    "ksl_moe_combine_stock": ([_P, _P, _P, _I64, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_act_to_down_order": ([_P, _I64, _I64, _P, _P], _I),
     "ksl_moe_layer_forward": ([_P, _I, _I64, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                                _I64, _I64, _I64, _I64, _I64, _I, _P, _I, _I64, _P, _SZ, _P], _I),
@@ -66,6 +72,7 @@ SIGNATURES = {
                                _P, _I64, _P, _SZ, _P], _I),
     "ksl_moe_ffn_ctl_bytes": ([_I64], _SZ),
     "ksl_moe_ffn": ([_P, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _P, _P, _P, _P], _I),
+    "ksl_moe_ffn_set_wait_limit": ([_I64, _I], _I),
     "ksl_moe_pack_gateup_bytes": ([_I64, _I64, _I64], _SZ),
     "ksl_moe_pack_gateup": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_pack_down_bytes": ([_I64, _I64, _I64], _SZ),

@@ -34,8 +34,14 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
                 const void* dn_z, int64_t E, int64_t H, int64_t I, void* out3, hipStream_t st, int layout,
                 int64_t nrows);
+const int32_t* ffn_error_word(const int32_t* ctl);
 
 namespace {
+
+// Output of a call whose expert FFN reported a failed wait (its error word,
+// read by the combine of the same call, is nonzero): every element NaN, so
+// that the result cannot pass for a normal one.
+__device__ __forceinline__ bool poisoned(const int32_t* __restrict__ err) { return err && *err != 0; }
 
 constexpr int kCombThreads = 256;
 
@@ -84,7 +90,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
                                                               const int32_t* __restrict__ inv,
                                                               const void* __restrict__ wv, int64_t T,
                                                               int topk, int64_t H, void* __restrict__ yv,
-                                                              int64_t ys) {
+                                                              int64_t ys, const int32_t* __restrict__ err) {
     typedef typename Elem<YD>::T YT;
     YT* y = static_cast<YT*>(yv);
     const int64_t hv = H / 8;
@@ -98,27 +104,124 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = static_cast<float>(static_cast<f16>(acc[j]));
     }
+    if (poisoned(err)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_nanf("");
+    }
     store8<YD>(y + t * ys + c0, acc);
 }
 
 template <int WD, bool F16P>
 int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w, int64_t T,
-                     int64_t topk, int64_t H, void* y, int64_t ys, hipStream_t st) {
+                     int64_t topk, int64_t H, void* y, int64_t ys, hipStream_t st, const int32_t* err) {
     const int64_t n = T * (H / 8);
     const unsigned grid = static_cast<unsigned>((n + kCombThreads - 1) / kCombThreads);
     const f16* o3 = static_cast<const f16*>(out3);
     switch (yd) {
         case KSL_DTYPE_BF16:
             hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_BF16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys);
+                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
             break;
         case KSL_DTYPE_F16:
             hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys);
+                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
             break;
         case KSL_DTYPE_F32:
             hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F32, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys);
+                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
+            break;
+        default:
+            return KSL_ERR_ARG;
+    }
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+
+// ---- the stock experts loop's combine -----------------------------------------
+// DiffusionGemmaTextExperts.forward (TF modeling_diffusion_gemma.py:578-588),
+// as kernels/pack_experts.py:44-62 runs it over the W4 linears: y starts at
+// zero in the hidden dtype; expert by expert in ascending id, each of its rows
+// adds term = YD(h * w[t, k]) to y[t] with one rounding to YD per add
+// (index_add_). h * w is the torch product of fp16 h and the routing weight:
+// in fp32 for fp32 or bf16 weights (type promotion), in fp16 for fp16 ones.
+// Per token the slots are taken in (expert id, slot) order; ids outside
+// [0, E) contribute nothing. One thread per 8 columns of one token.
+constexpr int kStockMaxTopk = 32;
+
+template <int WD, int YD>
+__global__ __launch_bounds__(kCombThreads) void combine_stock_kernel(const f16* __restrict__ out3,
+                                                                    const int32_t* __restrict__ inv,
+                                                                    const int64_t* __restrict__ ids, int64_t E,
+                                                                    const void* __restrict__ wv, int64_t T, int topk,
+                                                                    int64_t H, void* __restrict__ yv, int64_t ys) {
+    typedef typename Elem<YD>::T YT;
+    typedef typename Elem<WD>::T WT;
+    const WT* w = static_cast<const WT*>(wv);
+    const int64_t hv = H / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kCombThreads + threadIdx.x;
+    const int64_t t = idx / hv;
+    if (t >= T) return;
+    const int64_t c0 = (idx - t * hv) * 8;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    int64_t prev_id = -1;
+    int prev_k = -1;
+    for (int r = 0; r < topk; ++r) {
+        // the next slot in (id, slot) order
+        int64_t best_id = INT64_MAX;
+        int best_k = -1;
+        for (int k = 0; k < topk; ++k) {
+            const int64_t id = ids[t * topk + k];
+            const bool after = id > prev_id || (id == prev_id && k > prev_k);
+            if (after && (id < best_id || (id == best_id && k < best_k))) {
+                best_id = id;
+                best_k = k;
+            }
+        }
+        prev_id = best_id;
+        prev_k = best_k;
+        if (best_id < 0 || best_id >= E) continue;
+        const int64_t row = inv[t * topk + best_k];
+        const f16x8 h = *reinterpret_cast<const f16x8*>(out3 + row * H + c0);
+        const float wk = Elem<WD>::load(w + t * topk + best_k);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // separately rounded product and sum, never contracted to an FMA
+            // (the reference multiplies, then index_add_ adds)
+#pragma clang fp contract(off)
+            float term = static_cast<float>(h[j]) * wk;
+            if (WD == KSL_DTYPE_F16) term = static_cast<float>(static_cast<f16>(term));
+            if (YD == KSL_DTYPE_BF16) {
+                acc[j] = bf16r(acc[j] + bf16r(term));
+            } else if (YD == KSL_DTYPE_F16) {
+                acc[j] = static_cast<float>(static_cast<f16>(acc[j] + static_cast<float>(static_cast<f16>(term))));
+            } else {
+                acc[j] = acc[j] + term;
+            }
+        }
+    }
+    store8<YD>(static_cast<YT*>(yv) + t * ys + c0, acc);
+}
+
+template <int WD>
+int launch_combine_stock_y(int yd, const f16* out3, const int32_t* inv, const int64_t* ids, int64_t E, const void* w,
+                           int64_t T, int64_t topk, int64_t H, void* y, int64_t ys, hipStream_t st) {
+    const int64_t n = T * (H / 8);
+    const unsigned grid = static_cast<unsigned>((n + kCombThreads - 1) / kCombThreads);
+    const int k = static_cast<int>(topk);
+    switch (yd) {
+        case KSL_DTYPE_BF16:
+            hipLaunchKernelGGL((combine_stock_kernel<WD, KSL_DTYPE_BF16>), dim3(grid), dim3(kCombThreads), 0, st, out3,
+                               inv, ids, E, w, T, k, H, y, ys);
+            break;
+        case KSL_DTYPE_F16:
+            hipLaunchKernelGGL((combine_stock_kernel<WD, KSL_DTYPE_F16>), dim3(grid), dim3(kCombThreads), 0, st, out3,
+                               inv, ids, E, w, T, k, H, y, ys);
+            break;
+        case KSL_DTYPE_F32:
+            hipLaunchKernelGGL((combine_stock_kernel<WD, KSL_DTYPE_F32>), dim3(grid), dim3(kCombThreads), 0, st, out3,
+                               inv, ids, E, w, T, k, H, y, ys);
             break;
         default:
             return KSL_ERR_ARG;
@@ -153,6 +256,7 @@ struct PostArgs {
     const uint16_t* wp;     // bf16 [H]: post_feedforward_layernorm weight
     const void* ls;         // layer scalar (one element) or null for 1
     uint16_t* y;            // bf16 [T, ys]
+    const int32_t* err;     // the expert FFN's error word, or null
     int64_t h1s, rs, ys;
     float eps2, eps;
     int topk, H, ls_dt;
@@ -216,13 +320,19 @@ __global__ __launch_bounds__(kPostMaxWaves * kWave) void combine_post_kernel(Pos
     raw_unpack8<BF>(wpv, wpf);
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = bf16r(bf16r(rf[j] + rms_apply<true>(s[j], r, wpf[j])) * ls);
+    if (poisoned(A.err)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = __builtin_nanf("");
+    }
     if (ok) store8<BF>(A.y + t * A.ys + c0, o);
 }
 
 }  // namespace
 
+// err: the expert FFN's error word of the same call (null: none).
 int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
-                   int64_t topk, int64_t H, void* y, int yd, int64_t ys, hipStream_t st, bool f16p = false) {
+                   int64_t topk, int64_t H, void* y, int yd, int64_t ys, hipStream_t st, bool f16p = false,
+                   const int32_t* err = nullptr) {
     if (!out3 || !inv || !w || !y) return T == 0 ? KSL_OK : KSL_ERR_ARG;
     if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0 || ys < H) return KSL_ERR_SHAPE;
     if (ys % 8 != 0 || reinterpret_cast<uintptr_t>(out3) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
@@ -230,16 +340,16 @@ int launch_combine(const void* out3, const int32_t* inv, const void* w, int wd, 
     if (T == 0) return KSL_OK;
     if (f16p) {
         switch (wd) {
-            case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
-            case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
-            case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, true>(yd, out3, inv, w, T, topk, H, y, ys, st);
+            case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, true>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
+            case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, true>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
+            case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, true>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
         }
         return KSL_ERR_ARG;
     }
     switch (wd) {
-        case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
-        case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
-        case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, false>(yd, out3, inv, w, T, topk, H, y, ys, st);
+        case KSL_DTYPE_F32: return launch_combine_y<KSL_DTYPE_F32, false>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
+        case KSL_DTYPE_F16: return launch_combine_y<KSL_DTYPE_F16, false>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
+        case KSL_DTYPE_BF16: return launch_combine_y<KSL_DTYPE_BF16, false>(yd, out3, inv, w, T, topk, H, y, ys, st, err);
     }
     return KSL_ERR_ARG;
 }
@@ -264,7 +374,7 @@ static int check_post(int64_t T, int64_t topk, int64_t H, int wd, const void* h1
 int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int wd, int64_t T,
                         int64_t topk, int64_t H, const void* h1, int64_t h1s, const void* res, int64_t rs,
                         const void* w2, float eps2, const void* wp, float eps, const void* ls, int ls_dt,
-                        void* y, int64_t ys, hipStream_t st) {
+                        void* y, int64_t ys, hipStream_t st, const int32_t* err = nullptr) {
     const int rc = check_post(T, topk, H, wd, h1, h1s, res, rs, w2, wp, ls, ls_dt, y, ys);
     if (rc || T == 0) return rc;
     if (!out3 || !inv || !w) return KSL_ERR_ARG;
@@ -279,6 +389,7 @@ int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int
     A.wp = static_cast<const uint16_t*>(wp);
     A.ls = ls;
     A.y = static_cast<uint16_t*>(y);
+    A.err = err;
     A.h1s = h1s;
     A.rs = rs;
     A.ys = ys;
@@ -361,6 +472,34 @@ extern "C" int ksl_moe_combine_v1(const void* out3, const int32_t* inv, const vo
                                static_cast<hipStream_t>(stream), true);
 }
 
+extern "C" int ksl_moe_combine_stock(const void* out3, const int32_t* inv, const int64_t* topk_ids, int64_t E,
+                                     const void* topk_w, int w_dtype, int64_t T, int64_t topk, int64_t H, void* y,
+                                     int y_dtype, int64_t y_stride, void* stream) {
+    using namespace ksl;
+    if (T < 0 || topk <= 0 || topk > kStockMaxTopk || E <= 0 || H <= 0 || H % 8 != 0 || y_stride < H)
+        return KSL_ERR_SHAPE;
+    if (T == 0) return KSL_OK;
+    if (!out3 || !inv || !topk_ids || !topk_w || !y) return KSL_ERR_ARG;
+    if (y_stride % 8 != 0 || reinterpret_cast<uintptr_t>(out3) % 16 || reinterpret_cast<uintptr_t>(y) % 16 ||
+        reinterpret_cast<uintptr_t>(topk_ids) % 8)
+        return KSL_ERR_ALIGN;
+    if (T * (H / 8) / kCombThreads >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    const f16* o3 = static_cast<const f16*>(out3);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (w_dtype) {
+        case KSL_DTYPE_F32:
+            return launch_combine_stock_y<KSL_DTYPE_F32>(y_dtype, o3, inv, topk_ids, E, topk_w, T, topk, H, y,
+                                                         y_stride, st);
+        case KSL_DTYPE_F16:
+            return launch_combine_stock_y<KSL_DTYPE_F16>(y_dtype, o3, inv, topk_ids, E, topk_w, T, topk, H, y,
+                                                         y_stride, st);
+        case KSL_DTYPE_BF16:
+            return launch_combine_stock_y<KSL_DTYPE_BF16>(y_dtype, o3, inv, topk_ids, E, topk_w, T, topk, H, y,
+                                                          y_stride, st);
+    }
+    return KSL_ERR_ARG;
+}
+
 extern "C" int ksl_moe_combine_post(const void* out3, const int32_t* inv, const void* topk_w, int w_dtype,
                                     int64_t T, int64_t topk, int64_t H, const void* h1, int64_t h1_stride,
                                     const void* residual, int64_t residual_stride, const void* post2_w,
@@ -411,7 +550,8 @@ extern "C" int ksl_moe_w4a16_forward(const void* hidden, int hidden_dtype, int64
     rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
                      E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
-    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st, false,
+                          ffn ? ffn_error_word(ctl) : nullptr);
 }
 
 namespace ksl {
@@ -440,7 +580,8 @@ static int layer_forward_on(char* ws, const void* x, int x_dtype, int64_t x_stri
     rc = run_experts(a16, sorted_rows, offsets, topk, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, dn_layout, gu_pack, dn_pack,
                      E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
-    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st);
+    return launch_combine(out3, inv, topk_w, w_dtype, T, topk, H, y, y_dtype, y_stride, st, false,
+                          ffn ? ffn_error_word(ctl) : nullptr);
 }
 
 static int layer_forward_check(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I, int act, int dn_layout) {
@@ -562,7 +703,8 @@ extern "C" int ksl_moe_block_forward(const void* x, int64_t x_stride, const void
                      E, H, I, act, out2, out3, ctl, T * topk, st);
     if (rc) return rc;
     return launch_combine_post(out3, inv, topk_w, w_dtype, T, topk, H, h1, h1_stride, x, x_stride, post2_w,
-                               post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st);
+                               post2_eps, post_w, post_eps, layer_scalar, ls_dtype, y, y_stride, st,
+                               ffn ? ffn_error_word(ctl) : nullptr);
 }
 
 extern "C" size_t ksl_moe_route_scratch_bytes(int64_t T, int64_t topk, int64_t E) {
@@ -584,7 +726,7 @@ extern "C" int ksl_moe_layer_route(const int64_t* topk_ids, int64_t T, int64_t t
                            norm_w_dtype, eps, H, a16, bcnt, static_cast<hipStream_t>(stream), nullptr, 0);
 }
 
-extern "C" int ksl_version(void) { return 5; }
+extern "C" int ksl_version(void) { return 6; }
 
 extern "C" const char* ksl_status_string(int status) {
     switch (status) {

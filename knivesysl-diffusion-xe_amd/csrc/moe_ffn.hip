@@ -75,7 +75,7 @@ constexpr int kDnTileB = 1024 + 128;      // per tile and 128-K slot: one block,
 constexpr int kDnTailB = 512 + 64;        // per tile, trailing 64-K group: half block, then (s, z)
 constexpr int kSlotW = 25600;           // pack bytes of a ring slot (>= 11 * 2176, 22 * 1152)
 constexpr int kPlanN = 8;               // plan ring entries
-constexpr int kMaxIdle = 1 << 18;       // empty cycles a unit may wait for its dependency
+constexpr int kMaxIdle = 1 << 18;       // empty cycles a unit may wait for its dependency (default)
 constexpr int kMaxE = 512;
 
 static_assert(kSlotW >= kGuT * kGuTileB && kSlotW >= kDnT * kDnTileB, "slot too small");
@@ -106,6 +106,8 @@ struct FfnArgs {
     int G;           // 128-K groups of H (gate/up slots per unit)
     int nfull, tail; // down slots per unit: I / 128 full, one 64-K tail when I % 128 == 64
     int n0;          // units taken statically (= gridDim.x): workgroup b starts with unit b
+    int max_idle;    // empty cycles a down unit waits for its expert's gate/up units before giving up
+    int force_wait;  // nonzero: every dependency counts as unmet (failure-handling tests)
 };
 
 template <int MTX>
@@ -723,7 +725,7 @@ __device__ void ffn_control(const FfnArgs& A, const Plan* plans_c, int* toks, in
     auto take_batch = [&]() {
         // the batch's results (the compiler's wait lands here)
         if (poll_in) {
-            dep_ok = ruf(poll_v) >= gu_units(nx.e);
+            dep_ok = !A.force_wait && ruf(poll_v) >= gu_units(nx.e);
             poll_in = false;
         }
         if (nx_state == kPulled) {
@@ -802,7 +804,7 @@ __device__ void ffn_control(const FfnArgs& A, const Plan* plans_c, int* toks, in
                 k_end = k;
                 return;
             } else {
-                if (nx_state == kDepWait && ++idle > kMaxIdle) {
+                if (nx_state == kDepWait && ++idle > A.max_idle) {
                     // bounded wait: record the error and let the unit run
                     if (lane == 0) __hip_atomic_store(errw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     nx_state = kReady;
@@ -1046,6 +1048,23 @@ constexpr int kFfnR = 4;    // ring slots (three in flight)
 
 size_t ffn_ctl_words(int64_t E) { return (static_cast<size_t>(E) + kCtlExpert0) * kCtlStride; }
 
+// The error word of a ctl array: nonzero after a launch whose bounded wait
+// gave up (its out2 / out3 are not to be trusted).
+const int32_t* ffn_error_word(const int32_t* ctl) { return ctl ? ctl + kCtlError * kCtlStride : nullptr; }
+
+// Process-wide wait limit of the down units' dependency wait, and the
+// failure-handling switch that makes every dependency count as unmet.
+static std::atomic<int> g_max_idle{kMaxIdle};
+static std::atomic<int> g_force_wait{0};
+
+int ffn_set_wait_limit(int64_t cycles, int force_wait) {
+    if (cycles < 0) cycles = kMaxIdle;
+    if (cycles > (int64_t(1) << 30)) return KSL_ERR_ARG;
+    g_max_idle.store(static_cast<int>(cycles), std::memory_order_relaxed);
+    g_force_wait.store(force_wait ? 1 : 0, std::memory_order_relaxed);
+    return KSL_OK;
+}
+
 bool ffn_supported(int64_t E, int64_t H, int64_t I, int64_t nrows) {
     return E > 0 && E <= kMaxE && H % 128 == 0 && I % 64 == 0 && H >= 128 && I >= 64 && nrows > 0 &&
            nrows <= 8192 && H <= 8192 && I <= 8192;
@@ -1080,6 +1099,8 @@ int launch_ffn(const void* a16, const int32_t* sorted_rows, const int32_t* offse
     A.G = static_cast<int>(H / 128);
     A.nfull = static_cast<int>(I / 128);
     A.tail = (I % 128) != 0;
+    A.max_idle = g_max_idle.load(std::memory_order_relaxed);
+    A.force_wait = g_force_wait.load(std::memory_order_relaxed);
     const int64_t first = E * A.ncb;  // chunk-0 gate/up units: every workgroup's first unit is one
     const int64_t grid = std::min<int64_t>(ffn_cus(), first);
     A.n0 = static_cast<int>(grid);
@@ -1116,6 +1137,10 @@ extern "C" int ksl_moe_ffn(const void* a16, const int32_t* sorted_rows, const in
     if (reinterpret_cast<uintptr_t>(ctl) % 4) return KSL_ERR_ALIGN;
     return ksl::launch_ffn(a16, sorted_rows, offsets, topk, gu_pack, dn_pack, E, H, I, act, out2, out3, ctl, T * topk,
                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ksl_moe_ffn_set_wait_limit(int64_t cycles, int force_wait) {
+    return ksl::ffn_set_wait_limit(cycles, force_wait);
 }
 
 extern "C" size_t ksl_moe_pack_gateup_bytes(int64_t E, int64_t H, int64_t I) {

@@ -847,6 +847,34 @@ __global__ __launch_bounds__(256) void unshuffle_ns_down_kernel(const uint8_t* _
     *reinterpret_cast<uint64_t*>(out + (static_cast<int64_t>(e) * H + nt * 64 + n) * ih + kb * 32 + 8 * m) = v;
 }
 
+// The reference layout to the MOE_NS down pack, preshuffle_T_dn
+// (kernels/fused_moe_w4_v2.py:186-197): per expert [I/2, H]; within 64-K
+// chunk kb, NS byte row kb*32 + j of column n = q[kb*64 + j] | q[kb*64 + 32 + j] << 4.
+// One workgroup per (expert, chunk, 64 columns): the 64 columns' 32-byte
+// chunk pieces go through LDS; each thread then writes 8 columns of one NS row.
+__global__ __launch_bounds__(256) void preshuffle_ns_down_kernel(const uint8_t* __restrict__ dn,
+                                                                 uint8_t* __restrict__ ns, int H, int I) {
+    __shared__ uint8_t tile[64][32];
+    const int nt = blockIdx.x, kb = blockIdx.y, e = blockIdx.z, t = threadIdx.x;
+    const int ih = I / 2;
+    {
+        const int n = t >> 2, m = t & 3;  // column n, chunk bytes 8m .. 8m+7
+        *reinterpret_cast<uint64_t*>(&tile[n][8 * m]) = *reinterpret_cast<const uint64_t*>(
+            dn + (static_cast<int64_t>(e) * H + nt * 64 + n) * ih + kb * 32 + 8 * m);
+    }
+    __syncthreads();
+    const int j = t >> 3, n8 = (t & 7) * 8;  // NS row j of the chunk, columns n8 .. n8+7
+    const int sh = 4 * (j & 1);
+    uint64_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t lo = (static_cast<uint32_t>(tile[n8 + i][j >> 1]) >> sh) & 15u;
+        const uint32_t hi = (static_cast<uint32_t>(tile[n8 + i][16 + (j >> 1)]) >> sh) & 15u;
+        v |= static_cast<uint64_t>(lo | (hi << 4)) << (8 * i);
+    }
+    *reinterpret_cast<uint64_t*>(ns + (static_cast<int64_t>(e) * ih + kb * 32 + j) * H + nt * 64 + n8) = v;
+}
+
 // Activation rows in plain column order -> the down kernel's activation
 // order (out2_store_index): thread i moves 8 consecutive columns of one row.
 __global__ __launch_bounds__(256) void act_to_down_order_kernel(const f16* __restrict__ src, int64_t rows, int I,
@@ -1019,6 +1047,22 @@ extern "C" int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t
     hipLaunchKernelGGL(unshuffle_ns_down_kernel,
                        dim3(static_cast<unsigned>(H / 64), static_cast<unsigned>(I / 64), static_cast<unsigned>(E)),
                        dim3(256), 0, static_cast<hipStream_t>(stream), ns_q, dn_q, static_cast<int>(H),
+                       static_cast<int>(I));
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+
+extern "C" int ksl_moe_preshuffle_ns_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* ns_q,
+                                          void* stream) {
+    using namespace ksl;
+    if (E <= 0 || H <= 0 || I <= 0 || H % 64 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
+    if (E > 65535 || I / 64 > 65535 || H / 64 > (int64_t(1) << 31) - 1) return KSL_ERR_SHAPE;
+    if (!dn_q || !ns_q) return KSL_ERR_ARG;
+    if (dn_q == ns_q) return KSL_ERR_ARG;  // out of place
+    if (reinterpret_cast<uintptr_t>(dn_q) % 8 || reinterpret_cast<uintptr_t>(ns_q) % 8) return KSL_ERR_ALIGN;
+    hipLaunchKernelGGL(preshuffle_ns_down_kernel,
+                       dim3(static_cast<unsigned>(H / 64), static_cast<unsigned>(I / 64), static_cast<unsigned>(E)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), dn_q, ns_q, static_cast<int>(H),
                        static_cast<int>(I));
     KSL_LAUNCH_CHECK();
     return KSL_OK;

@@ -88,8 +88,55 @@ int launch_quantize(const void* w, int64_t rows, int64_t K, int64_t gs, uint8_t*
     return KSL_OK;
 }
 
+// dequant_w4 (kernels/w4a16.py:35-48): W[n, k] = fp16((q - zero) * scale) with
+// the difference and the product taken in fp32 (the reference promotes the
+// fp16 nibble values against fp32 scale / zero), rounded once to fp16. One
+// thread per 8 consecutive K of one row (4 packed bytes in, 16 bytes out);
+// group_size % 8 == 0, so the 8 share one (scale, zero).
+__global__ __launch_bounds__(256) void dequant_w4_kernel(const uint8_t* __restrict__ q, const f16* __restrict__ scale,
+                                                         const f16* __restrict__ zero, int64_t rows, int K, int gs,
+                                                         f16* __restrict__ out) {
+    const int64_t per_row = K / 8;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= rows * per_row) return;
+    const int64_t r = i / per_row;
+    const int c8 = static_cast<int>(i - r * per_row) * 8;
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(q + r * (K / 2) + c8 / 2);
+    const int64_t gi = r * (K / gs) + c8 / gs;
+    const float s = static_cast<float>(scale[gi]);
+    const float z = static_cast<float>(zero[gi]);
+    f16x8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float qj = static_cast<float>((w >> (4 * j)) & 15u);
+        v[j] = static_cast<f16>(__fmul_rn(__fsub_rn(qj, z), s));
+    }
+    *reinterpret_cast<f16x8*>(out + r * K + c8) = v;
+}
+
 }  // namespace
 }  // namespace ksl
+
+extern "C" int ksl_dequant_w4(const uint8_t* qpacked, const void* scale, const void* zero, int64_t rows, int64_t K,
+                              int64_t group_size, void* out, void* stream) {
+    using namespace ksl;
+    if (rows < 0 || K <= 0 || group_size <= 0) return KSL_ERR_SHAPE;
+    if (group_size % 8 != 0 || K % group_size != 0 || K > (int64_t(1) << 30)) return KSL_ERR_SHAPE;
+    if (rows == 0) return KSL_OK;
+    if (!qpacked || !scale || !zero || !out) return KSL_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(qpacked) % 4 || reinterpret_cast<uintptr_t>(out) % 16 ||
+        reinterpret_cast<uintptr_t>(scale) % 2 || reinterpret_cast<uintptr_t>(zero) % 2)
+        return KSL_ERR_ALIGN;
+    const int64_t n = rows * (K / 8);
+    const int64_t grid = (n + 255) / 256;
+    if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    hipLaunchKernelGGL(dequant_w4_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), qpacked, static_cast<const f16*>(scale),
+                       static_cast<const f16*>(zero), rows, static_cast<int>(K), static_cast<int>(group_size),
+                       static_cast<f16*>(out));
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
 
 extern "C" int ksl_quantize_w4(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t group_size,
                                uint8_t* qpacked, void* scale, void* zero, void* stream) {

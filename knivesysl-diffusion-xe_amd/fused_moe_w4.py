@@ -63,7 +63,19 @@ def fused_moe_w4(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torc
     exp.act_fn applied in torch between the gate/up and down GEMMs. `exp`
     carries gu_q/gu_s/gu_z, dn_q/dn_s/dn_z in the packed format
     (kernels/pack_experts.py:96-97) and act_fn."""
-    from .fused_moe_w4_v2 import _check_weights, _same_device, dn_layout
+    return expert_rows_forward(hidden, exp, topk_ids, topk_w, combine="v1")
+
+
+@torch.no_grad()
+def expert_rows_forward(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torch.Tensor,
+                        combine: str = "v1") -> torch.Tensor:
+    """Routing, gate/up, exp.act_fn(gate) * up in torch, down, then the
+    combine: "v1" the v1 fp16-product combine (kernels/fused_moe_w4.py:125-127,
+    ksl_moe_combine_v1), "stock" the stock experts loop's expert-ordered
+    index_add_ (kernels/pack_experts.py:44-62, ksl_moe_combine_stock)."""
+    from .fused_moe_w4_v2 import _check_weights, _same_device, check_zero_points_once, dn_layout
+    if combine not in ("v1", "stock"):
+        raise ValueError(f"unknown combine {combine!r}")
     T, H = hidden.shape
     tk = topk_ids.shape[1]
     E, twoI, _ = exp.gu_q.shape
@@ -72,6 +84,7 @@ def fused_moe_w4(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torc
     if not hidden.is_cuda:
         raise ValueError("hidden must be on the GPU")
     _check_weights(exp, E, H, I)
+    check_zero_points_once(exp)
     _same_device(hidden.device, topk_ids=topk_ids, topk_w=topk_w, gu_q=exp.gu_q, dn_q=exp.dn_q)
     _lib.dtype_code(hidden.dtype), _lib.dtype_code(topk_w.dtype)  # fp32 / fp16 / bf16, else TypeError
     dev = hidden.device
@@ -105,6 +118,11 @@ def fused_moe_w4(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: torc
     _lib.check(lib.ksl_moe_down(_lib.ptr(out2d), _lib.ptr(offsets), _lib.ptr(exp.dn_q), _lib.ptr(exp.dn_s),
                                 _lib.ptr(exp.dn_z), E, H, I, Nexp, _lib.ptr(out3), dn_layout(exp), st),
                "ksl_moe_down")
-    _lib.check(lib.ksl_moe_combine_v1(_lib.ptr(out3), _lib.ptr(inv), _lib.ptr(w), _lib.dtype_code(w.dtype), T, tk,
-                                      H, _lib.ptr(y), _lib.dtype_code(y.dtype), H, st), "ksl_moe_combine_v1")
+    if combine == "v1":
+        _lib.check(lib.ksl_moe_combine_v1(_lib.ptr(out3), _lib.ptr(inv), _lib.ptr(w), _lib.dtype_code(w.dtype), T,
+                                          tk, H, _lib.ptr(y), _lib.dtype_code(y.dtype), H, st), "ksl_moe_combine_v1")
+    else:
+        _lib.check(lib.ksl_moe_combine_stock(_lib.ptr(out3), _lib.ptr(inv), _lib.ptr(ids), E, _lib.ptr(w),
+                                             _lib.dtype_code(w.dtype), T, tk, H, _lib.ptr(y),
+                                             _lib.dtype_code(y.dtype), H, st), "ksl_moe_combine_stock")
     return y

@@ -18,20 +18,25 @@ the output is bit-identical run to run.
 Differences from the reference, on purpose:
 - SiLU-gated experts are supported next to tanh-GELU (the reference asserts
   tanh-GELU, :291-308, :332).
-- The preshuffled down pack (MOE_NS, :180-245) is not run as such: a
-  module flagged `dn_ns` (enable_ns_down, :200-206) has its down weights
-  converted on first sight to the tiled layout, the same nibbles regrouped
-  in the order the down kernel loads them (enable_tiled_down, flagged by
-  `dn_tiled`). Results are those of the plain pack.
+- The preshuffled down pack (MOE_NS, :180-245) is not run as such.
+  enable_ns_down (:200-206) installs, at load time, the down layout this
+  build's kernel streams instead: the tiled layout, the same nibbles
+  regrouped in the order the down kernel loads them (enable_tiled_down,
+  flagged by `dn_tiled`). A module that arrives flagged `dn_ns` (an NS pack
+  made elsewhere) is converted on its first forward. Results are those of
+  the plain pack. preshuffle_T_dn still writes the NS bytes exactly (for
+  checkpoints or comparisons).
 - zero-points must be integers in [0, 15] (what quantize_w4 writes,
   kernels/w4a16.py:28). check_zero_points verifies it with one host sync;
   the load-time helpers (enable_tiled_down, enable_pack, pack_experts'
-  repack_experts and load helpers) call it, so the forward itself never
-  synchronises the host and can be captured from its first call.
+  repack_experts and load helpers) call it. A module none of them saw is
+  checked on its first forward outside graph capture; under capture the
+  check is skipped (no host sync is allowed there).
 """
 from __future__ import annotations
 
 import os
+import weakref
 
 import torch
 
@@ -163,6 +168,17 @@ def check_zero_points(exp) -> None:
     exp._ksl_zeros_checked = True
 
 
+def check_zero_points_once(exp) -> None:
+    """check_zero_points on a module that no load-time helper has checked,
+    unless the current stream is being captured into a graph (a host sync
+    is not allowed there: the check is then left to a later eager call)."""
+    if getattr(exp, "_ksl_zeros_checked", False):
+        return
+    if torch.cuda.is_current_stream_capturing():
+        return
+    check_zero_points(exp)
+
+
 @torch.no_grad()
 def unshuffle_ns_down(ns_q: torch.Tensor) -> torch.Tensor:
     """The MOE_NS down pack [E, I/2, H] (kernels/fused_moe_w4_v2.py:187-197)
@@ -182,6 +198,27 @@ def _same_device(dev, **tensors) -> None:
     for name, t in tensors.items():
         if t is not None and t.device != dev:
             raise ValueError(f"{name} is on {t.device}, the activations on {dev}")
+
+
+def _cache_get(cache: dict | None, key, *sources):
+    """The cached value for key if every source tensor it was made from is
+    still the very tensor given (a freed tensor's address can be reused by a
+    new allocation: the key alone would bind another module's data)."""
+    if cache is None:
+        return None
+    entry = cache.get(key)
+    if entry is None:
+        return None
+    refs, value = entry
+    if len(refs) != len(sources) or any(r() is not src for r, src in zip(refs, sources)):
+        del cache[key]
+        return None
+    return value
+
+
+def _cache_put(cache: dict | None, key, value, *sources) -> None:
+    if cache is not None:
+        cache[key] = (tuple(weakref.ref(src) for src in sources), value)
 
 
 def dn_layout(exp) -> int:
@@ -211,18 +248,46 @@ def enable_tiled_down(exp, cache: dict | None = None):
     experts of a layer, kernels/load_w4_checkpoint.py:56-59) keep sharing one."""
     if getattr(exp, "dn_tiled", False):
         return exp
-    key = (exp.dn_q.data_ptr(), str(exp.dn_q.device))
-    t = None if cache is None else cache.get(key)
+    src = exp.dn_q
+    key = (src.data_ptr(), str(src.device), bool(getattr(exp, "dn_ns", False)))
+    t = _cache_get(cache, key, src)
     if t is None:
-        ref = unshuffle_ns_down(exp.dn_q) if getattr(exp, "dn_ns", False) else exp.dn_q
+        ref = unshuffle_ns_down(src) if getattr(exp, "dn_ns", False) else src
         t = tiled_down(ref)
-        if cache is not None:
-            cache[key] = t
+        _cache_put(cache, key, t, src)
     exp.dn_q = t
     exp.dn_ns = False
     exp.dn_tiled = True
     check_zero_points(exp)
     return exp
+
+
+@torch.no_grad()
+def preshuffle_T_dn(qpacked: torch.Tensor, BK: int = 64) -> torch.Tensor:
+    """kernels/fused_moe_w4_v2.py:186-197: the down pack [E, N, K/2] in the
+    reference layout -> the MOE_NS pack [E, K/2, N] (within each BK = 64 chunk
+    byte j = q[k0 + j] | q[k0 + 32 + j] << 4, transposed), byte for byte, by
+    one launch (ksl_moe_preshuffle_ns_down)."""
+    if BK != 64:
+        raise ValueError("the MOE_NS pack is defined for BK = 64 (the down group size)")
+    E, N, Kh = qpacked.shape
+    if not qpacked.is_cuda or qpacked.dtype != torch.uint8 or not qpacked.is_contiguous():
+        raise ValueError("qpacked must be a contiguous uint8 tensor on the GPU")
+    out = torch.empty(E, Kh, N, dtype=torch.uint8, device=qpacked.device)
+    rc = _lib.load().ksl_moe_preshuffle_ns_down(_lib.ptr(qpacked), E, N, 2 * Kh, _lib.ptr(out),
+                                                _lib.stream_of(qpacked))
+    _lib.check(rc, "ksl_moe_preshuffle_ns_down")
+    return out
+
+
+def enable_ns_down(exp, cache: dict | None = None):
+    """kernels/fused_moe_w4_v2.py:200-206: the load-time switch to the faster
+    down pack, in place and idempotent. The reference installs its MOE_NS
+    pack for its NS kernel; this build installs the layout its own down kernel
+    streams (enable_tiled_down: the same nibbles regrouped, the plain pack's
+    results), with `cache` keeping shared buffers shared. A module whose dn_q
+    already is an NS pack (dn_ns) is converted from it."""
+    return enable_tiled_down(exp, cache)
 
 
 @torch.no_grad()
@@ -254,12 +319,12 @@ def enable_pack(exp, cache: dict | None = None):
     sharing one pack."""
     if getattr(exp, "gu_pack", None) is not None and getattr(exp, "dn_pack", None) is not None:
         return exp
+    srcs = (exp.gu_q, exp.dn_q)
     key = (exp.gu_q.data_ptr(), exp.dn_q.data_ptr(), str(exp.gu_q.device))
-    t = None if cache is None else cache.get(key)
+    t = _cache_get(cache, key, *srcs)
     if t is None:
         t = pack_weights(exp)
-        if cache is not None:
-            cache[key] = t
+        _cache_put(cache, key, t, *srcs)
     exp.gu_pack, exp.dn_pack = t
     return exp
 
@@ -287,6 +352,7 @@ def fused_moe_w4_v2(hidden: torch.Tensor, exp, topk_ids: torch.Tensor, topk_w: t
     if not hasattr(exp, "_ksl_act"):
         _check_act(exp)
     _check_weights(exp, E, K, I)
+    check_zero_points_once(exp)
     if topk_ids.shape[0] != T or tuple(topk_w.shape) != (T, tk):
         raise ValueError("topk_ids / topk_w must be [T, topk]")
     dev = hidden.device

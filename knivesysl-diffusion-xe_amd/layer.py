@@ -21,7 +21,8 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .fused_moe_w4_v2 import _check_act, _check_weights, _same_device, dn_layout, fused_moe_w4_v2, moe_workspace, pack_ptrs
+from .fused_moe_w4_v2 import (_check_act, _check_weights, _same_device, check_zero_points_once, dn_layout,
+                              fused_moe_w4_v2, moe_workspace, pack_ptrs)
 from .fused_rmsnorm import fused_rmsnorm
 
 STAGES = ("route_norm", "gateup", "down", "combine")
@@ -33,6 +34,7 @@ def _prepare(exp, x, E, H, I):
     if not getattr(exp, "_act_checked", False) or not hasattr(exp, "_ksl_act"):
         _check_act(exp)
     _check_weights(exp, E, H, I)
+    check_zero_points_once(exp)
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("moe_layer takes bf16 or fp16 activations")
     if x.stride(1) != 1 or x.stride(0) % 8 != 0 or x.data_ptr() % 16 != 0:
@@ -104,6 +106,15 @@ class LayerRunner:
                                    dtype=torch.int32, device=device)
         # counters of the one-launch expert FFN: zero once, left zero by every launch
         self.ctl = torch.zeros(int(self.lib.ksl_moe_ffn_ctl_bytes(E)) // 4, dtype=torch.int32, device=device)
+
+    def ffn_error(self) -> bool:
+        """True if a one-launch FFN stage of this runner gave up a bounded wait
+        (its out2 / out3 were then not to be trusted). The word latches until
+        clear_ffn_error(); reading it synchronises with the device."""
+        return bool(self.ctl[_lib.FFN_ERROR_WORD].item())
+
+    def clear_ffn_error(self) -> None:
+        self.ctl[_lib.FFN_ERROR_WORD] = 0
 
     def stages(self, exp) -> tuple:
         return STAGES_FFN if self._use_ffn(exp) else STAGES

@@ -8,10 +8,13 @@ each layer's shard once and registers the same six tensors on every experts
 module of that layer (modules named "...layers.<N>.experts"), binds the
 fused forward, then runs the load-time repack once per shared tensor (the
 tiled down layout, optionally the one-launch FFN pack) so the modules keep
-sharing. Shards are read with safetensors only (no pickle).
+sharing. Shards are read with safetensors only (no pickle). As the
+reference's load_w4 does (kernels/load_w4_checkpoint.py:38-41, :100), a
+directory without w4_meta.json is refused: it is not a dg-w4a16 checkpoint.
 """
 from __future__ import annotations
 
+import json
 import pathlib
 import re
 
@@ -48,6 +51,20 @@ def expert_shards(ckpt) -> dict:
     return found
 
 
+def checkpoint_meta(ckpt) -> dict:
+    """w4_meta.json of a dg-w4a16 checkpoint directory (its "format" names the
+    pack format); AssertionError with the reference's message if absent."""
+    ckpt = pathlib.Path(ckpt).resolve()
+    assert (ckpt / "w4_meta.json").exists(), (
+        f"{ckpt} is not a dg-w4a16 checkpoint (no w4_meta.json). Point this at the directory "
+        f"holding model.safetensors + experts_*.safetensors, not at the bf16 base model."
+    )
+    meta = json.loads((ckpt / "w4_meta.json").read_text())
+    if not isinstance(meta, dict):
+        raise ValueError(f"{ckpt / 'w4_meta.json'}: expected a JSON object")
+    return meta
+
+
 @torch.no_grad()
 def bind_expert_shards(model, ckpt, device="cuda", tile_down: bool = True, pack: bool = False) -> int:
     """Register each layer's six packed buffers on all of its experts modules
@@ -55,6 +72,7 @@ def bind_expert_shards(model, ckpt, device="cuda", tile_down: bool = True, pack:
     load time (tile_down: the tiled down layout; pack: also the one-launch
     expert FFN pack). Returns the number of modules bound."""
     from safetensors.torch import load_file
+    checkpoint_meta(ckpt)  # a dg-w4a16 checkpoint, else AssertionError
     by_layer = experts_by_layer(model)
     shards = expert_shards(ckpt)
     missing = sorted(set(by_layer) - set(shards))

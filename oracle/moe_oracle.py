@@ -418,6 +418,83 @@ def combine_v1(out3: np.ndarray, inv: np.ndarray, topk_w: np.ndarray) -> np.ndar
     return acc.astype(np.float16)
 
 
+def combine_stock(out3: np.ndarray, inv: np.ndarray, topk_ids: np.ndarray, topk_w: np.ndarray, E: int,
+                  out_dtype: str = "bf16") -> np.ndarray:
+    """The stock experts loop's combine (kernels/pack_experts.py:44-62, TF
+    modeling_diffusion_gemma.py:578-588): final = zeros in the hidden dtype;
+    for each expert in ascending id, over its (slot, token) pairs,
+    final.index_add_(0, token, (h * w[token, slot]).to(dtype)) with h =
+    out3[inv[token*tk + slot]] fp16. h * w is fp32 for fp32 / bf16 weights,
+    fp16 for fp16 weights (torch's promotion); each add is one rounding to the
+    hidden dtype. out_dtype "bf16" returns bf16 bits, "f16" / "f32" arrays."""
+    T, tk = topk_ids.shape
+    H = out3.shape[1]
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    inv2 = np.asarray(inv).reshape(T, tk)
+    if out_dtype == "bf16":
+        rnd = lambda v: bf16_to_f32(f32_to_bf16(v))  # noqa: E731
+    elif out_dtype == "f16":
+        rnd = lambda v: v.astype(np.float16).astype(np.float32)  # noqa: E731
+    else:
+        rnd = lambda v: v.astype(np.float32)  # noqa: E731
+    acc = np.zeros((T, H), dtype=np.float32)
+    for e in range(E):
+        ks, ts = np.nonzero((ids == e).T)  # torch.where over the [tk, T] mask: slot-major
+        if ts.size == 0:
+            continue
+        # a token listed twice for one expert is added once per slot, in slot order
+        rank = np.zeros(ts.size, dtype=np.int64)
+        count: dict = {}
+        for i, t in enumerate(ts.tolist()):
+            rank[i] = count.get(t, 0)
+            count[t] = rank[i] + 1
+        for r in range(int(rank.max()) + 1):
+            sel = rank == r
+            t, k = ts[sel], ks[sel]
+            h = out3[inv2[t, k]]
+            wk = topk_w[t, k]
+            if topk_w.dtype == np.float16:
+                term = (h.astype(np.float32) * wk.astype(np.float32)[:, None]).astype(np.float16).astype(np.float32)
+            else:
+                term = h.astype(np.float32) * wk.astype(np.float32)[:, None]
+            acc[t] = rnd(acc[t] + rnd(term))
+    if out_dtype == "bf16":
+        return f32_to_bf16(acc)
+    return acc.astype(np.float16) if out_dtype == "f16" else acc
+
+
+def _v1_rows(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, topk_ids: np.ndarray, act16):
+    """out3 rows [T*tk, H] fp16 of the v1 / packed-loop expert stages (row
+    t*tk + k for slot k of token t): out1 = fp16(A @ Wgu^T), out2 =
+    fp16(act16(gate) * up) (fused_moe_w4.py:117-119; pack_experts.py:56-58),
+    out3 = fp16(out2 @ Wd^T)."""
+    T, H = hidden_f32.shape
+    E, twoI, _ = gu_q.shape
+    I = twoI // 2
+    tk = topk_ids.shape[1]
+    flat = np.asarray(topk_ids, dtype=np.int64).reshape(-1)
+    a16 = hidden_f32.astype(np.float16)
+    out3_rows = np.zeros((T * tk, H), dtype=np.float16)
+    for e in range(E):
+        r = np.nonzero(flat == e)[0]
+        if r.size == 0:
+            continue
+        out1 = gateup_raw(a16[r // tk], dequant_w4(gu_q[e], gu_s[e], gu_z[e], GU_GS))
+        gate, up = out1[:, :I], out1[:, I:]
+        o2 = (np.asarray(act16(gate), dtype=np.float16).astype(np.float32) * up.astype(np.float32)).astype(np.float16)
+        out3_rows[r] = down(o2, dequant_w4(dn_q[e], dn_s[e], dn_z[e], DN_GS))
+    return out3_rows
+
+
+def moe_forward_stock(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
+                      topk_ids: np.ndarray, topk_w: np.ndarray, act16, out_dtype: str = "bf16"):
+    """One packed_experts_forward call (kernels/pack_experts.py:44-62): the
+    v1 expert stages then combine_stock."""
+    T, tk = topk_ids.shape
+    rows = _v1_rows(hidden_f32, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z, topk_ids, act16)
+    return combine_stock(rows, np.arange(T * tk), topk_ids, topk_w, gu_q.shape[0], out_dtype)
+
+
 def moe_forward_v1(hidden_f32: np.ndarray, gu_q, gu_s, gu_z, dn_q, dn_s, dn_z,
                    topk_ids: np.ndarray, topk_w: np.ndarray, act16):
     """One fused_moe_w4 call (fused_moe_w4.py:104-128) with the activation

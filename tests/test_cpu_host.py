@@ -98,3 +98,18 @@ def test_moe_block_forward_checks_dtypes_and_patches_layers():
     assert mb.patch_moe_blocks(model, verbose=False) == 1
     assert model[0].forward.__func__ is mb.layer_forward
     assert "forward" not in model[1].__dict__
+
+
+def test_checkpoint_meta_refuses_a_directory_without_w4_meta(tmp_path):
+    """kernels/load_w4_checkpoint.py:38-41: a directory without w4_meta.json
+    is not a dg-w4a16 checkpoint (checked before anything is loaded)."""
+    lw = load_mod("load_w4")
+    with pytest.raises(AssertionError, match="not a dg-w4a16 checkpoint"):
+        lw.checkpoint_meta(tmp_path)
+    with pytest.raises(AssertionError, match="not a dg-w4a16 checkpoint"):
+        lw.bind_expert_shards(torch.nn.Module(), tmp_path, device="cpu")
+    (tmp_path / "w4_meta.json").write_text('{"format": "dg-w4a16-v1", "group_size": 128}')
+    assert lw.checkpoint_meta(tmp_path)["format"] == "dg-w4a16-v1"
+    (tmp_path / "w4_meta.json").write_text('[1, 2]')
+    with pytest.raises(ValueError):
+        lw.checkpoint_meta(tmp_path)

@@ -632,3 +632,71 @@ def test_moe_forward_v1_matches_v2_for_the_same_activation():
     o1 = mo.gateup_raw(a16, w16)
     assert np.array_equal(o1[:, :I], mo._mm_f32(a16, w16[:I]).astype(np.float16))
     assert np.array_equal(o1[:, I:], mo._mm_f32(a16, w16[I:]).astype(np.float16))
+
+
+# ---------------------------------------------------------------- packed experts loop
+def _stock_loop_torch(out3, inv, ids, w, E, dtype):
+    """The reference's packed loop (kernels/pack_experts.py:44-62) evaluated by
+    torch on the CPU, with h of (token, slot) = out3[inv[token * tk + slot]]."""
+    import torch.nn.functional as F
+    T, tk = ids.shape
+    o3 = torch.from_numpy(out3)
+    inv2 = torch.from_numpy(np.asarray(inv).reshape(T, tk))
+    idx = torch.from_numpy(ids)
+    tw = torch.from_numpy(w)
+    final = torch.zeros(T, out3.shape[1], dtype=dtype)
+    expert_mask = F.one_hot(idx, num_classes=E).permute(2, 1, 0)
+    hit = torch.greater(expert_mask.sum(dim=(-1, -2)), 0).nonzero()
+    for expert_idx in hit:
+        e = expert_idx[0]
+        top_k_pos, token_idx = torch.where(expert_mask[e])
+        h = o3[inv2[token_idx, top_k_pos]]
+        h = h * tw[token_idx, top_k_pos, None]
+        final.index_add_(0, token_idx, h.to(final.dtype))
+    return final
+
+
+@pytest.mark.parametrize("wdt", [np.float32, np.float16])
+@pytest.mark.parametrize("out", ["bf16", "f16", "f32"])
+def test_combine_stock_equals_torch_on_the_reference_loop(wdt, out):
+    """combine_stock against torch's own CPU evaluation of the reference's
+    expression (one_hot mask, per-expert index_add_ of (h * w).to(dtype)), bit
+    for bit: experts in ascending id, one rounding per add. A plain slot-order
+    fp32 sum rounded once differs (the per-add roundings show)."""
+    g = np.random.default_rng(41)
+    T, tk, H, E = 48, 8, 128, 16
+    out3 = (3.0 * g.standard_normal((T * tk, H))).astype(np.float16)
+    inv = g.permutation(T * tk)
+    ids = np.stack([g.permutation(E)[:tk] for _ in range(T)]).astype(np.int64)
+    w = g.dirichlet(np.ones(tk), size=T).astype(wdt)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[out]
+    ref = _stock_loop_torch(out3, inv, ids, w, E, tdt)
+    got = mo.combine_stock(out3, inv, ids, w, E, out)
+    if out == "bf16":
+        assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+    elif out == "f16":
+        assert np.array_equal(got.view(np.uint16), ref.numpy().view(np.uint16))
+    else:
+        assert np.array_equal(got.view(np.uint32), ref.numpy().view(np.uint32))
+    if out == "bf16":
+        once = mo.f32_to_bf16(mo.combine_fma(out3, inv, w.astype(np.float32)))
+        assert not np.array_equal(got, once)
+
+
+def test_combine_stock_known_answer():
+    """Hand-worked bf16 case: token 0 routed to experts 3 (slot 0, w = 1) and
+    1 (slot 1, w = 1) with h = 256 and h = 1.5. Expert 1 goes first: 0 + 1.5
+    = 1.5; then 1.5 + 256 = 257.5, which bf16 (8-bit mantissa, ulp 2 at 256)
+    rounds to 258 (half to even between 256 + 2 and 256). Slot order would
+    give 256 + 1.5 = 257.5 -> 258 as well; with h = 1.0 instead, 1 + 256 =
+    257 -> 256 (tie to even) either way, so also: expert 1 term 0.75 and a
+    third expert 0 term 0.75 first: 0.75 + 0.75 = 1.5, + 256 -> 258, while
+    256 + 0.75 = 256.75 -> 256, + 0.75 -> 256 in slot order."""
+    out3 = np.array([[256.0], [0.75], [0.75]], np.float16)
+    ids = np.array([[3, 1, 0]], np.int64)
+    w = np.ones((1, 3), np.float32)
+    got = mo.bf16_to_f32(mo.combine_stock(out3, np.arange(3), ids, w, 4, "bf16"))
+    assert float(got[0, 0]) == 258.0
+    # skipped ids (>= E) contribute nothing
+    got2 = mo.bf16_to_f32(mo.combine_stock(out3, np.arange(3), np.array([[3, 9, 0]], np.int64), w, 4, "bf16"))
+    assert float(got2[0, 0]) == 256.0

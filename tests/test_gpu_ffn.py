@@ -190,3 +190,51 @@ def test_layer_runner_ffn_stages_match_the_fused_call(gpu):
     torch.cuda.synchronize()
     for r in ys:
         assert np.array_equal(bf16_bits(r), bf16_bits(y))
+
+
+def test_failed_wait_poisons_the_call(gpu):
+    """A down unit whose bounded wait for its expert's gate/up units gives up
+    sets the error word, and the fused forwards then return NaN for that call
+    instead of normal-looking output. The failure is forced from the host
+    (every dependency counts as unmet, a bound of 4 empty ring cycles): each
+    down unit waits out the bound and runs, every workgroup finishes normally.
+    The next call with the default bound is clean and equals the first."""
+    lib = load_pkg()._lib
+    L = lib.load()
+    v2 = load_mod("fused_moe_w4_v2")
+    layer = load_mod("layer")
+    pkg = load_pkg()
+    wl = load_mod("workloads")
+    T, tk, E, H, I = 64, 8, 16, 512, 192
+    exp = wl.make_experts(E, H, I, 95, act="silu").to(gpu)
+    v2.enable_pack(exp)
+    x, nw, ids, w = wl.layer_inputs(T, 96, E=E, k=tk, H=H)
+    xg, nwg, idsg, wg = x.to(gpu), nw.to(gpu), ids.to(gpu), w.to(gpu)
+    hidden = pkg.fused_rmsnorm(xg, nwg, 1e-6)
+    y_ok = layer.moe_layer(xg, nwg, 1e-6, exp, idsg, wg)
+    f_ok = v2.fused_moe_w4_v2(hidden, exp, idsg, wg)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y_ok).any() and not torch.isnan(f_ok).any()
+    runner = layer.LayerRunner(T, tk, E, H, I, gpu)
+    lib.check(L.ksl_moe_ffn_set_wait_limit(4, 1), "ksl_moe_ffn_set_wait_limit")
+    try:
+        print(f"forced failed wait: moe_layer / fused_moe_w4_v2 / LayerRunner T={T} E={E} H={H} I={I}", flush=True)
+        y_bad = layer.moe_layer(xg, nwg, 1e-6, exp, idsg, wg)
+        f_bad = v2.fused_moe_w4_v2(hidden, exp, idsg, wg)
+        runner.run(xg, nwg, 1e-6, exp, idsg, wg)
+        torch.cuda.synchronize()
+    finally:
+        lib.check(L.ksl_moe_ffn_set_wait_limit(-1, 0), "ksl_moe_ffn_set_wait_limit")
+    assert torch.isnan(y_bad).all(), "moe_layer returned normal-looking output after a failed wait"
+    assert torch.isnan(f_bad).all(), "fused_moe_w4_v2 returned normal-looking output after a failed wait"
+    # the standalone launch latches the error word in the caller's counters
+    assert runner.ffn_error(), "the runner's error word was not set"
+    c = runner.ctl.cpu().numpy()
+    c[CTL_STRIDE * 1] = 0
+    assert not c.any(), "counters other than the error word not cleared"
+    # a normal call afterwards: the routing clears the word, same bits as before
+    y_again = layer.moe_layer(xg, nwg, 1e-6, exp, idsg, wg)
+    torch.cuda.synchronize()
+    assert torch.equal(y_again.view(torch.int16), y_ok.view(torch.int16))
+    # out-of-range bounds are refused
+    assert L.ksl_moe_ffn_set_wait_limit(1 << 31, 0) == lib.ERR_ARG

@@ -191,6 +191,7 @@ def test_bind_expert_shards_shares_one_tensor_per_layer(gpu, tmp_path):
         save_file({f"{prefix}.{b}": getattr(exp, b).contiguous() for b in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z")},
                   str(tmp_path / f"experts_{i:03d}.safetensors"))
     model = _Model(L).to(gpu)
+    (tmp_path / "w4_meta.json").write_text('{"format": "dg-w4a16-v1"}')
     assert lw.bind_expert_shards(model, tmp_path, device=gpu, pack=True) == 2 * L
     hidden = wl.make_hidden(T, H, 72).to(gpu)
     ids, w = wl.make_routing(T, E, tk, 73)
