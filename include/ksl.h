@@ -221,8 +221,8 @@ int ksl_moe_gateup_act(const void* a16, const int32_t* sorted_rows, const int32_
                        int64_t E, int64_t H, int64_t I, int act, void* out2, void* stream);
 
 /* Grouped W4 down GEMM. Replaces _down_kernel (kernels/fused_moe_w4_v2.py:146-177).
- * out3 fp16 [T*topk, H] row per sorted slot, natural column order, 8-byte
- * aligned (written 4 columns per store). nrows:
+ * out3 fp16 [T*topk, H] row per sorted slot, natural column order, 16-byte
+ * aligned (written 8 columns per store). nrows:
  * the routed rows (T*topk), which size the grid (above 8192 routed rows each
  * workgroup takes a block of at most 64 rows of one expert, so that a heavy
  * expert spreads over many workgroups). dn_layout as in ksl_moe_w4a16_forward. */
@@ -283,15 +283,25 @@ int ksl_moe_unshuffle_ns_down(const uint8_t* ns_q, int64_t E, int64_t H, int64_t
 int ksl_moe_preshuffle_ns_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* ns_q,
                                void* stream);
 
-/* Load-time repack of the down weights into the layout the down kernel loads
- * (the reference's precedent is the preshuffled down pack,
- * kernels/fused_moe_w4_v2.py:187-206). Out of place, same size as
- * dn_q [E, H, I/2]. Within each 16-row tile (base address unchanged): unit u
- * < I/128 is 1 KB, 16 bytes per lane l = c*16 + col: row col, bytes
- * u*64 + c*16 .. +16; then for I % 128 == 64 a 512-byte tail, 8 bytes per
- * lane: row col, bytes (I/128)*64 + c*8 .. +8. A pure permutation of bytes.
- * H % 16 == 0, I % 64 == 0. */
-int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled, void* stream);
+/* Load-time repack of the down buffers into the layout the down kernel
+ * streams (the reference's precedent is the preshuffled down pack,
+ * kernels/fused_moe_w4_v2.py:187-206). Out of place, into
+ * ksl_moe_repack_down_bytes(E, H, I) bytes (16-byte aligned):
+ *   - first E*H*I/2 bytes: the tiled weights, a pure permutation of dn_q
+ *     [E, H, I/2]. Within each 16-row tile (base address unchanged): unit
+ *     u < I/128 is 1 KB, 16 bytes per lane l = c*16 + col: row col, bytes
+ *     u*64 + c*16 .. +16; then for I % 128 == 64 a 512-byte tail, 8 bytes per
+ *     lane: row col, bytes (I/128)*64 + c*8 .. +8;
+ *   - then the (scale, zero) pair table: per tile T, group g < I/64 and row
+ *     col of the tile, the uint32 (scale bits | zero bits << 16) at index
+ *     (T*(I/64) + g)*16 + col.
+ * A buffer passed to the forwards as dn_q with KSL_DN_LAYOUT_TILED must be
+ * one written by this call (the down kernel reads the pair table behind the
+ * E*H*I/2 weight bytes; dn_s and dn_z still serve the other kernels).
+ * dn_s / dn_z fp16 [E, H, I/64]. H % 16 == 0, I % 64 == 0. */
+size_t ksl_moe_repack_down_bytes(int64_t E, int64_t H, int64_t I);
+int ksl_moe_repack_down(const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t E, int64_t H, int64_t I,
+                        uint8_t* dn_q_tiled, void* stream);
 
 /* Gate/up + activation and down of every expert in ONE persistent launch over
  * the pack layout (the stage that ksl_moe_w4a16_forward runs between routing

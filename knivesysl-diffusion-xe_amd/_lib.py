@@ -53,7 +53,8 @@ SIGNATURES = {
     "ksl_moe_unshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_preshuffle_ns_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_dequant_w4": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
-    "ksl_moe_repack_down": ([_P, _I64, _I64, _I64, _P, _P], _I),
+    "ksl_moe_repack_down_bytes": ([_I64, _I64, _I64], _SZ),
+    "ksl_moe_repack_down": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I),
     "ksl_moe_combine": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_combine_v1": ([_P, _P, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),
     "ksl_moe_combine_stock": ([_P, _P, _P, _I64, _P, _I, _I64, _I64, _I64, _P, _I, _I64, _P], _I),

@@ -39,6 +39,7 @@
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "ksl_common.h"
 
@@ -484,22 +485,27 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // --------------------------------------------------------------------- down
 // Register-streamed kernel. A workgroup of kDnWaves waves owns one expert and
 // a range of its output columns (the expert's H columns split over
-// ceil(#CUs / E) workgroups); the expert's activation rows (out2, up to 64 per
-// chunk) and the scale / zero rows of the workgroup's columns are copied into
-// LDS once (direct global->LDS loads), so each activation row is read once
-// per workgroup. Every wave then walks its 16-column tiles (tiles w, w+12, ...)
-// with the weights in registers, double buffered: the next tile's 16 rows x
-// I/2 bytes are loaded while the current tile is decoded and multiplied, and
-// all waves do MFMA and nibble decoding (down's decode, with the scale folded
-// in, costs as much VALU time as the bytes take to stream).
+// ceil(#CUs / E) workgroups). The expert's activation rows (out2, up to 64 per
+// chunk) are copied into LDS once per chunk (direct global->LDS loads). Every
+// wave then walks pairs of 16-column tiles (pairs w, w + kDnWaves, ...): each
+// lane loads its weight words and the scale / zero-point of its groups for
+// both tiles of the next pair straight into registers, by ordinary loads that
+// the compiler tracks and waits for, while the current pair is decoded and
+// multiplied. The two tiles of a pair share every activation fragment read
+// from LDS (half the LDS reads of one tile at a time). Nothing is staged
+// before a wave's first pair but the activations, and no load is issued past
+// a wave's last pair (each weight byte is fetched once).
 //
 // K mapping: one 16-byte load per lane and 128-K block, lane (col, c) holding
 // row col, nibbles 32c .. 32c+31 of the block: MFMA step i takes nibbles
-// 32c + 8i .. +8, the 128-group activation order (out2_store_index); the scale
-// group of lane group c is 2*g2 + c/2. A trailing 64-K group (I % 128 == 64)
-// takes an 8-byte load, the 64-group order. B = fp16((q - z) * s), the
-// reference's own dequantised weight (kernels/fused_moe_w4_v2.py:172-175).
-constexpr int kDnWaves = 12;
+// 32c + 8i .. +8, the 128-group order of the activations (out2_store_index);
+// the lane's 32 nibbles of a block lie in one 64-K quantisation group,
+// 2*g2 + c/2. A trailing 64-K group (I % 128 == 64) takes an 8-byte load per
+// lane, the 64-group order. B = fp16((q - z) * s), the reference's own
+// dequantised weight (kernels/fused_moe_w4_v2.py:172-175), accumulated in
+// fp32 in K order, so each output element sees the same MFMA sequence as the
+// row-block kernel of large routings (moe_rbgemm.hip).
+constexpr int kDnWaves = 8;
 constexpr int kDnMaxMt = 4;  // 16-row M tiles per row chunk of down (64 rows)
 constexpr int kDnThreads = kDnWaves * kWave;
 constexpr int kDnMaxG = 16;  // I <= 1024
@@ -523,105 +529,184 @@ struct DnArgs {
     const f16* dn_s;
     const f16* dn_z;
     f16* out3;
+    const uint32_t* sz;     // tiled layout: the (scale, zero) pair table after the tiled weights
     int H, I, nsplit, tpw;  // tpw: 16-column tiles per workgroup
+    int early;              // weights of the first pair are requested before the routing is read
 };
 
-// LDS: activation blocks [kDnMaxMt][2G] (1 KB each, frag_pos order), then the
-// s rows and the z rows ([nrows][G] fp16 each) of the workgroup's columns.
-inline size_t dn_lds_bytes(int G, int nrows) {
-    return static_cast<size_t>(kDnMaxMt) * 2 * G * kBlk + static_cast<size_t>(nrows) * G * 4;
-}
+// LDS: activation blocks [kDnMaxMt][2G] (1 KB each, frag_pos order), then
+// one output staging area per wave (two 16-row M tiles of a pair's 32
+// columns, kDnOutRow bytes per row).
+constexpr int kDnOutRow = 80;  // 64 bytes of a row + 16 of padding (2-way bank conflicts at most)
+constexpr int kDnOutWave = 2 * 16 * kDnOutRow;
+__host__ __device__ inline size_t dn_act_bytes(int G) { return static_cast<size_t>(kDnMaxMt) * 2 * G * kBlk; }
+inline size_t dn_lds_bytes(int G) { return dn_act_bytes(G) + static_cast<size_t>(kDnWaves) * kDnOutWave; }
 
-template <int G2, bool TAIL>
-struct DnW {
+// One lane's part of one tile: G2 16-byte weight words, the 8-byte tail, and
+// the (scale, zero-point) of the lane's group in each 128-K block and of the
+// tail group: one (s | z << 16) word each in the tiled layout (the pair
+// table), two 16-bit values (in 32-bit registers: as 16-bit array elements
+// they were kept in scratch memory) in the reference layout.
+template <int G2, bool TAIL, int LAYOUT>
+struct DnTile {
+    static constexpr int NG = G2 + (TAIL ? 1 : 0);
     u32x4 q[G2];
     u32x2 t[TAIL ? 1 : 0];
+    uint32_t sz[LAYOUT == kDnTiled ? NG : 0];
+    uint32_t s[LAYOUT == kDnTiled ? 0 : NG], z[LAYOUT == kDnTiled ? 0 : NG];
+    __device__ __forceinline__ f16 scale(int j) const {
+        if constexpr (LAYOUT == kDnTiled) return __builtin_bit_cast(f16x2, sz[j])[0];
+        else return __builtin_bit_cast(f16, static_cast<uint16_t>(s[j]));
+    }
+    __device__ __forceinline__ f16 zero(int j) const {
+        if constexpr (LAYOUT == kDnTiled) return __builtin_bit_cast(f16x2, sz[j])[1];
+        else return __builtin_bit_cast(f16, static_cast<uint16_t>(z[j]));
+    }
 };
 
-// A tile's weights: G2 16-byte loads and, with TAIL, one 8-byte load. Issued
-// as asm so that the compiler's conservative wait at the tile loop's head
-// (vmcnt(0), which would drain the next tile's prefetch) is not inserted; the
-// waits are explicit (dn_wait_w), the compiler-placed ones can only wait more.
-// The compiler takes the registers as written at the asm: nothing may copy
-// them before dn_wait_w, so a buffer enters the tile loop only once complete
-// and is otherwise loaded and used inside one loop iteration pair (checked in
-// the generated code: no register copies of a loading buffer).
+// Compile-time loop: f(integral_constant<int, 0>) .. f(integral_constant<int, N-1>).
+template <int N, typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
+// Per-lane byte offsets of a tile's loads, the same for every tile (kept in
+// registers across the walk, so that a fetch only changes wave-uniform bases).
+struct DnLane {
+    int q;    // weight words (+ g2 * 1024 tiled, + g2 * 64 reference)
+    int t;    // the tail word
+    int sz;   // the lane's (scale, zero) of 128-K block g2 (+ g2 * 128 tiled, + g2 * 4 reference)
+    int szt;  // the tail group's (scale, zero)
+};
+
 template <int G2, bool TAIL, int LAYOUT>
-__device__ __forceinline__ void dn_load_w(DnW<G2, TAIL>& w, const uint8_t* tbase, int col, int c, int rb) {
-    if constexpr (LAYOUT == kDnTiled) {
-        // non-temporal: each weight byte is read once per launch (about 1 us
-        // faster at the 256-token layer than the cached load; the same hint on
-        // gate/up's direct-to-LDS loads costs 15 us there)
-        const uint8_t* p = tbase + (c * 16 + col) * 16;
-#pragma unroll
-        for (int g2 = 0; g2 < G2; ++g2)
-            asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(w.q[g2]) : "v"(p + g2 * 1024) : "memory");
-        if constexpr (TAIL) {
-            const uint8_t* pt = tbase + G2 * 1024 + (c * 16 + col) * 8;
-            asm volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(w.t[0]) : "v"(pt) : "memory");
-        }
-    } else {
-        const uint8_t* p = tbase + col * rb + c * 16;
-#pragma unroll
-        for (int g2 = 0; g2 < G2; ++g2)
-            asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(w.q[g2]) : "v"(p), "i"(g2 * 64) : "memory");
-        if constexpr (TAIL) {
-            const uint8_t* pt = tbase + col * rb + G2 * 64 + c * 8;
-            asm volatile("global_load_dwordx2 %0, %1, off nt" : "=v"(w.t[0]) : "v"(pt) : "memory");
-        }
-    }
-}
-
-// Wait until the loads of w have landed, N memory operations issued after
-// them allowed in flight; the empty asm orders every use of w after the wait.
-template <int N, int G2, bool TAIL>
-__device__ __forceinline__ void dn_wait_w(DnW<G2, TAIL>& w) {
-    vm_wait<N>();
-#pragma unroll
-    for (int g2 = 0; g2 < G2; ++g2) asm volatile("" : "+v"(w.q[g2]));
-    if constexpr (TAIL) asm volatile("" : "+v"(w.t[0]));
-}
-
-template <int G2, bool TAIL, int MT>
-__device__ __forceinline__ void dn_tile(const DnW<G2, TAIL>& w, f32x4 (&acc)[MT], const char* __restrict__ a_lds,
-                                        const f16* __restrict__ srow, const f16* __restrict__ zrow, int c, int fo,
-                                        const NibConsts& kn) {
+__device__ __forceinline__ DnLane dn_lane(int I, int col, int c) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-#pragma unroll
-    for (int g2 = 0; g2 < G2; ++g2) {
-        const int grp = 2 * g2 + (c >> 1);
-        const f16 sv = srow[grp];
-        const ZeroPair zc = zero_pair(zrow[grp]);
-        // decode here, not where the load lands (decoded nibbles take 4x the registers)
-        u32x4 wq = w.q[g2];
-        asm volatile("" : "+v"(wq));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f16x8 b = nib8_dequant(wq[i], zc, f16x2{sv, sv}, kn);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + g2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(b, a, acc[t]);
-            }
+    const int rb = I >> 1;
+    if constexpr (LAYOUT == kDnTiled)
+        return DnLane{(c * 16 + col) * 16, G2 * 1024 + (c * 16 + col) * 8, ((c >> 1) * 16 + col) * 4,
+                      (2 * G2 * 16 + col) * 4};
+    else
+        return DnLane{col * rb + c * 16, col * rb + G2 * 64 + c * 8, (col * G + (c >> 1)) * 2, (col * G + 2 * G2) * 2};
+}
+
+template <typename T>
+__device__ __forceinline__ T ld_nt(const uint8_t* base, int off) {
+    return __builtin_nontemporal_load(reinterpret_cast<const T*>(base + off));
+}
+
+// Requests tile `row` (its first dn row: expert * H + column) into w:
+// ordinary non-temporal loads, which the compiler waits for before the first
+// use of each register.
+template <int G2, bool TAIL, int LAYOUT>
+__device__ __forceinline__ void dn_fetch(DnTile<G2, TAIL, LAYOUT>& w, const DnArgs& A, int64_t row,
+                                         const DnLane& ln) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
+    // wave-uniform bases, lane offsets from ln
+    const uint8_t* tb = A.dn_q + row * (A.I >> 1);
+    if constexpr (LAYOUT == kDnTiled) {
+        // pair table: tile (row / 16), group g, column col at ((tile * G + g) * 16 + col)
+        const uint8_t* pb = reinterpret_cast<const uint8_t*>(A.sz + (row >> 4) * (G * 16));
+        static_for<G2>([&](auto j) { w.q[j] = ld_nt<u32x4>(tb, ln.q + j * 1024); });
+        if constexpr (TAIL) w.t[0] = ld_nt<u32x2>(tb, ln.t);
+        static_for<G2>([&](auto j) { w.sz[j] = ld_nt<uint32_t>(pb, ln.sz + j * 128); });
+        if constexpr (TAIL) w.sz[G2] = ld_nt<uint32_t>(pb, ln.szt);
+    } else {
+        const uint8_t* sb = reinterpret_cast<const uint8_t*>(A.dn_s + row * G);
+        const uint8_t* zb = reinterpret_cast<const uint8_t*>(A.dn_z + row * G);
+        static_for<G2>([&](auto j) { w.q[j] = ld_nt<u32x4>(tb, ln.q + j * 64); });
+        if constexpr (TAIL) w.t[0] = ld_nt<u32x2>(tb, ln.t);
+        static_for<G2>([&](auto j) {
+            w.s[j] = ld_nt<uint16_t>(sb, ln.sz + j * 4);
+            w.z[j] = ld_nt<uint16_t>(zb, ln.sz + j * 4);
+        });
+        if constexpr (TAIL) {
+            w.s[G2] = ld_nt<uint16_t>(sb, ln.szt);
+            w.z[G2] = ld_nt<uint16_t>(zb, ln.szt);
         }
-        // one 128-K block at a time: the other waves hide its LDS latency, and
-        // hoisting every block's operands would exceed the register budget
-        __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (TAIL) {
-        const f16 sv = srow[2 * G2];
-        const ZeroPair zc = zero_pair(zrow[2 * G2]);
-        u32x2 wt = w.t[0];
-        asm volatile("" : "+v"(wt));
+}
+
+// Both tiles of a pair against two M tiles of activations: every activation
+// fragment read from LDS feeds one MFMA of each tile. (A chunk with an odd
+// number of M tiles computes one tile more than it has: its LDS blocks hold
+// other rows, and its outputs are dropped at the store. The launch time is
+// that of the workgroups whose experts have two M tiles, so the spare MFMAs of
+// one-tile experts cost no time.)
+template <int G2, bool TAIL, int LAYOUT>
+__device__ __forceinline__ void dn_pair_mma(const DnTile<G2, TAIL, LAYOUT>& w0, const DnTile<G2, TAIL, LAYOUT>& w1,
+                                            f32x4 (&acc0)[2], f32x4 (&acc1)[2], const char* __restrict__ a_lds,
+                                            int fo, const NibConsts& kn) {
+    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
+    auto step = [&](const f16x8& b0, const f16x8& b1, int blk) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const f16x8 b = nib8_dequant(wt[i], zc, f16x2{sv, sv}, kn);
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + G2 * 4 + i) * kBlk + fo);
-                acc[t] = mfma16x16x32(b, a, acc[t]);
-            }
+        for (int t = 0; t < 2; ++t) {
+            const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + blk) * kBlk + fo);
+            acc0[t] = mfma16x16x32(b0, a, acc0[t]);
+            acc1[t] = mfma16x16x32(b1, a, acc1[t]);
         }
+    };
+    // the weight words pass through an empty asm, so that the decode happens
+    // here, in each pass, block by block: decoded weights (four times the
+    // registers of the words) are neither hoisted nor kept for a later pass
+    static_for<G2>([&](auto g2) {
+        const f16 s0 = w0.scale(g2), s1 = w1.scale(g2);
+        const ZeroPair z0 = zero_pair(w0.zero(g2)), z1 = zero_pair(w1.zero(g2));
+        u32x4 q0 = w0.q[g2], q1 = w1.q[g2];
+        asm volatile("" : "+v"(q0), "+v"(q1));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            step(nib8_dequant(q0[i], z0, f16x2{s0, s0}, kn), nib8_dequant(q1[i], z1, f16x2{s1, s1}, kn), g2 * 4 + i);
+        // one 128-K block at a time: hoisting every block's operands would
+        // exceed the register budget
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (TAIL) {
+        const f16 s0 = w0.scale(G2), s1 = w1.scale(G2);
+        const ZeroPair z0 = zero_pair(w0.zero(G2)), z1 = zero_pair(w1.zero(G2));
+        u32x2 q0 = w0.t[0], q1 = w1.t[0];
+        asm volatile("" : "+v"(q0), "+v"(q1));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            step(nib8_dequant(q0[i], z0, f16x2{s0, s0}, kn), nib8_dequant(q1[i], z1, f16x2{s1, s1}, kn), G2 * 4 + i);
+    }
+}
+
+// A pair's outputs for two M tiles. The weights are the MFMA's A operand and
+// the activations its B operand, so each accumulator is its tile transposed:
+// lane (col, c) holds row col of the M tile, the tile's output columns 4c ..
+// 4c+3. They go through the wave's LDS staging area (row-major, the pair's 32
+// columns per row) and out as 16 bytes per lane, four lanes per row: 64
+// contiguous bytes per row and one store per M tile. Rows past the chunk, or
+// a second tile past the workgroup's last, take an out-of-range offset
+// (dropped by the buffer store).
+__device__ __forceinline__ void dn_store_pair(const f32x4 (&acc0)[2], const f32x4 (&acc1)[2], char* o_lds,
+                                              __amdgpu_buffer_rsrc_t out, int H, int colw, bool second, int mrows,
+                                              int lane, int row0) {
+    const int col = lane & 15, c = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const f16x4 v0{static_cast<f16>(acc0[t][0]), static_cast<f16>(acc0[t][1]), static_cast<f16>(acc0[t][2]),
+                       static_cast<f16>(acc0[t][3])};
+        const f16x4 v1{static_cast<f16>(acc1[t][0]), static_cast<f16>(acc1[t][1]), static_cast<f16>(acc1[t][2]),
+                       static_cast<f16>(acc1[t][3])};
+        char* rowp = o_lds + (t * 16 + col) * kDnOutRow;
+        *reinterpret_cast<f16x4*>(rowp + c * 8) = v0;
+        *reinterpret_cast<f16x4*>(rowp + 32 + c * 8) = v1;
+    }
+    // lane (r = lane / 4, part = lane % 4): 16 bytes of row r, columns 8 * part ..
+    const int r = lane >> 2, part = lane & 3;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(o_lds + (t * 16 + r) * kDnOutRow + part * 16);
+        const int row = t * 16 + r;  // row0 + row of the chunk; mrows counted from row0
+        const bool ok = row < mrows && (second || part < 2);
+        const uint32_t off = ok ? static_cast<uint32_t>(((row0 + row) * H + colw + 8 * part) * 2) : kDropOffset;
+        __builtin_amdgcn_raw_buffer_store_b128(v, out, off, 0, 0);
     }
 }
 
@@ -641,142 +726,86 @@ __device__ __forceinline__ void dn_stage_a(const DnArgs& A, char* a_lds, int sta
     }
 }
 
-
-
-// One tile: MT M tiles x 16 columns. The weights are the MFMA's A operand and
-// the activations its B operand, so the accumulator is the tile transposed:
-// lane (col, c) holds row col of the M tile, output columns 4c .. 4c+3, and
-// writes them with one 8-byte store (out3 is 8-byte aligned, H % 64 == 0).
-// The stores have no branches (rows past the chunk, or a
-// repeated tile, take an out-of-range offset), so every wave issues the same
-// number of memory operations per tile and the waits on the prefetched
-// weights are exact.
-template <int G2, bool TAIL, int MT>
-__device__ __forceinline__ void dn_do_tile(const DnW<G2, TAIL>& w, const char* a_lds, const f16* s_lds,
-                                           const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int tile,
-                                           int colw, bool valid, int mrows, int col, int c, int fo,
-                                           const NibConsts& kn) {
-    constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-    f32x4 acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int rl = tile * 16 + col;  // row of dn within the workgroup's columns
-    dn_tile<G2, TAIL, MT>(w, acc, a_lds, s_lds + rl * G, z_lds + rl * G, c, fo, kn);
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const int row = t * 16 + col;
-        const uint32_t off = valid && row < mrows ? static_cast<uint32_t>((row * H + colw + tile * 16 + 4 * c) * 2)
-                                                  : kDropOffset;
-        const f16x4 v{static_cast<f16>(acc[t][0]), static_cast<f16>(acc[t][1]), static_cast<f16>(acc[t][2]),
-                      static_cast<f16>(acc[t][3])};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), out, off, 0, 0);
-    }
-}
-
-// A wave's tiles of one chunk: tiles wave + k*kDnWaves, k < nmine, weights of
-// tile k+1 loaded while tile k is computed. Loads are unconditional (past the
-// last tile they repeat it: an L2 hit), a repeated tile's stores are dropped,
-// so between a buffer's loads and its use exactly the other buffer's loads and
-// one tile's MT stores are issued (on entry w0 has landed already).
-template <int G2, bool TAIL, int MT, int LAYOUT>
-__device__ __forceinline__ void dn_tiles(DnW<G2, TAIL>& w0, DnW<G2, TAIL>& w1, const uint8_t* wrow, int rb,
-                                         int nmine, int wave, const char* a_lds, const f16* s_lds,
-                                         const f16* z_lds, __amdgpu_buffer_rsrc_t out, int H, int colw, int mrows,
-                                         int col, int c, int fo, const NibConsts& kn) {
-    constexpr int kAfter = G2 + (TAIL ? 1 : 0) + MT;
-    for (int k = 0; k < nmine; k += 2) {
-        const int k1 = k + 1 < nmine ? k + 1 : nmine - 1;
-        const int k2 = k + 2 < nmine ? k + 2 : nmine - 1;
-        dn_load_w<G2, TAIL, LAYOUT>(w1, wrow + static_cast<int64_t>(wave + k1 * kDnWaves) * 16 * rb, col, c, rb);
-        dn_wait_w<kAfter>(w0);
-        dn_do_tile<G2, TAIL, MT>(w0, a_lds, s_lds, z_lds, out, H, wave + k * kDnWaves, colw, true, mrows, col, c,
-                                 fo, kn);
-        // odd count: tile k was the wave's last. w1's repeated load is waited
-        // for here, so its registers stay w1's until it has landed
-        // (wave-uniform branch)
-        if (k + 1 >= nmine) {
-            dn_wait_w<0>(w1);
-            break;
-        }
-        dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave + k2 * kDnWaves) * 16 * rb, col, c, rb);
-        dn_wait_w<kAfter>(w1);
-        dn_do_tile<G2, TAIL, MT>(w1, a_lds, s_lds, z_lds, out, H, wave + k1 * kDnWaves, colw, k + 1 < nmine, mrows,
-                                 col, c, fo, kn);
-    }
-}
-
+// Each wave walks pairs of 16-column tiles of the workgroup (pair p = wave +
+// k*kDnWaves: tiles 2p and 2p+1; an odd last tile pairs with itself, its
+// second outputs dropped) for one chunk of mt M tiles: the pair's weights are
+// requested, then decoded and multiplied as they arrive. Latency is hidden
+// by the other waves of the SIMD rather than by a second register buffer (a
+// second buffer, measured, was not faster: the decode, the MFMAs with their
+// LDS reads and the stores already keep the SIMD busy while a wave waits).
+// The M tiles go in passes of at most two over the same weight registers
+// (accumulators for more would not fit), so a chunk of three or four M tiles
+// decodes its weights twice but streams them once.
 template <int G2, bool TAIL, int LAYOUT>
 __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
+    constexpr int MTX = kDnMaxMt;
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
-    // M tiles per chunk: four need more than the 168 registers of 12 waves
-    // once a tile's weights take G2 >= 6 128-K units (I >= 768)
-    constexpr int MTX = G2 >= 6 ? 2 : kDnMaxMt;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
     const int e = bid / A.nsplit;
     const int h = bid - e * A.nsplit;
-    const int start = A.offsets[e];
-    const int M = A.offsets[e + 1] - start;
     const int col0 = h * A.tpw * 16;
     const int ncols = A.H - col0 < A.tpw * 16 ? A.H - col0 : A.tpw * 16;
-    if (M <= 0 || ncols <= 0) return;
+    if (ncols <= 0) return;
     const int ntiles = ncols >> 4;
+    const int npairs = (ntiles + 1) >> 1;
     const int wave = wave_id();
+    const int npw = wave < npairs ? (npairs - 1 - wave) / kDnWaves + 1 : 0;
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
     const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
     const int fo = frag_pos(col, c) * 16;
     const NibConsts kn = nib_consts();
-    char* a_lds = lds;
-    f16* s_lds = reinterpret_cast<f16*>(lds + kDnMaxMt * 2 * G * kBlk);
-    f16* z_lds = s_lds + ncols * G;
     const int64_t row0 = static_cast<int64_t>(e) * A.H + col0;  // first dn row of the workgroup
-    const int rb = A.I >> 1;
-    const uint8_t* wrow = A.dn_q + row0 * rb;  // the workgroup's first tile
-    // 1. scale / zero rows and the first chunk's activations into LDS
-    {
-        const int nq = ncols * G / 8;  // 16-byte chunks per block
-        const char* ssrc = reinterpret_cast<const char*>(A.dn_s + row0 * G);
-        const char* zsrc = reinterpret_cast<const char*>(A.dn_z + row0 * G);
-        for (int q0 = wave * kWave; q0 < 2 * nq; q0 += kDnWaves * kWave) {
-            const int q = q0 + lane;
-            if (q < 2 * nq) dma16(q < nq ? ssrc + q * 16 : zsrc + (q - nq) * 16, reinterpret_cast<char*>(s_lds) + q0 * 16);
-        }
-        const int mrows = M < 16 * MTX ? M : 16 * MTX;
-        dn_stage_a<G2, TAIL>(A, a_lds, start, 0, mrows, (mrows + 15) >> 4, wave, rr, ch);
+    char* o_lds = lds + dn_act_bytes(G) + wave * kDnOutWave;
+    using Tile = DnTile<G2, TAIL, LAYOUT>;
+    Tile x0, x1;
+    const DnLane ln = dn_lane<G2, TAIL, LAYOUT>(A.I, col, c);
+    auto fetch = [&](int k) {
+        const int p = wave + k * kDnWaves;
+        const int t1i = 2 * p + 1 < ntiles ? 2 * p + 1 : 2 * p;
+        dn_fetch<G2, TAIL, LAYOUT>(x0, A, row0 + 32 * p, ln);
+        dn_fetch<G2, TAIL, LAYOUT>(x1, A, row0 + 16 * t1i, ln);
+    };
+    // most experts have rows: the first pair's weights go out before the
+    // routing is read
+    const bool early = A.early && npw > 0;
+    if (early) fetch(0);
+    const int start = A.offsets[e];
+    const int M = A.offsets[e + 1] - start;
+    if (M <= 0) {
+        vm_wait<0>();  // early loads land before the wave ends
+        return;
     }
-    // 2. the first tile's weights, then wait for the LDS copies only
-    DnW<G2, TAIL> w0, w1;
-    if (wave < ntiles) dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, col, c, rb);
-    vm_wait<0>();
-    dma_barrier();
-    const int nmine = wave < ntiles ? (ntiles - 1 - wave) / kDnWaves + 1 : 0;
     for (int m0 = 0; m0 < M; m0 += 16 * MTX) {
         const int mrows = M - m0 < 16 * MTX ? M - m0 : 16 * MTX;
         const int mt = (mrows + 15) >> 4;
-        if (m0 > 0) {
-            __syncthreads();  // every wave is done with the previous chunk's activations
-            dn_stage_a<G2, TAIL>(A, a_lds, start, m0, mrows, mt, wave, rr, ch);
-            if (wave < ntiles) dn_load_w<G2, TAIL, LAYOUT>(w0, wrow + static_cast<int64_t>(wave) * 16 * rb, col, c, rb);
-            vm_wait<0>();
-            dma_barrier();
-        }
+        if (m0 > 0) __syncthreads();  // every wave is done with the previous chunk's activations
+        dn_stage_a<G2, TAIL>(A, lds, start, m0, mrows, mt, wave, rr, ch);
+        vm_wait<0>();
+        dma_barrier();
         const __amdgpu_buffer_rsrc_t out =
             raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
-#define KSL_DN_TILES(MT_)                                                                                      \
-    dn_tiles<G2, TAIL, MT_, LAYOUT>(w0, w1, wrow, rb, nmine, wave, a_lds, s_lds, z_lds, out, A.H, col0, mrows, col, c, \
-                                    fo, kn)
-        if (mt == 1) {
-            KSL_DN_TILES(1);
-        } else if (MTX == 2 || mt == 2) {
-            KSL_DN_TILES(2);
-        } else if constexpr (MTX == 4) {
-            if (mt == 3) KSL_DN_TILES(3);
-            else KSL_DN_TILES(4);
+        for (int k = 0; k < npw; ++k) {
+            if (k > 0 || !(m0 == 0 && early)) fetch(k);
+            const int p = wave + k * kDnWaves;
+            // two straight-line passes, not a loop (a loop kept both tiles'
+            // weights and every pass temporary live at once: spills)
+            auto pass = [&](int t0) {
+                f32x4 acc0[2], acc1[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    acc0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    acc1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+                dn_pair_mma<G2, TAIL, LAYOUT>(x0, x1, acc0, acc1, lds + t0 * 2 * G * kBlk, fo, kn);
+                dn_store_pair(acc0, acc1, o_lds, out, A.H, col0 + 32 * p, 2 * p + 1 < ntiles, mrows - 16 * t0, lane,
+                              t0 * 16);
+            };
+            pass(0);
+            if (mt > 2) pass(2);
         }
-#undef KSL_DN_TILES
     }
-    vm_wait<0>();  // the last (repeated) prefetch lands before the wave ends
 }
 
 template <int G2, bool TAIL>
@@ -790,6 +819,20 @@ int launch_down_g(const DnArgs& A, unsigned grid, size_t lds, int layout, hipStr
         hipLaunchKernelGGL((down_kernel<G2, TAIL, kDnRef>), dim3(grid), dim3(kDnThreads), lds, st, A);
     KSL_LAUNCH_CHECK();
     return KSL_OK;
+}
+
+// The (scale, zero) pair table of the tiled layout: per 16-row tile T and
+// group g, the 16 rows' (scale | zero << 16) at ((T * G + g) * 16 + col).
+__global__ __launch_bounds__(256) void pair_scales_kernel(const uint16_t* __restrict__ s,
+                                                          const uint16_t* __restrict__ z, int64_t ntiles, int G,
+                                                          uint32_t* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= ntiles * G * 16) return;
+    const int64_t t = i / (G * 16);
+    const int r = static_cast<int>(i - t * G * 16);
+    const int g = r >> 4, col = r & 15;
+    const int64_t src = (t * 16 + col) * G + g;
+    out[i] = static_cast<uint32_t>(s[src]) | (static_cast<uint32_t>(z[src]) << 16);
 }
 
 // The tiled down layout from the reference one: one thread per 16-byte unit
@@ -938,9 +981,7 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
 }
 
 // Column split of the down launch: each expert's H/16 column tiles go to
-// nsplit workgroups of tpw tiles, enough workgroups to fill the CUs and few
-// enough tiles that their scale / zero rows fit in LDS beside the
-// activations (the static LDS reserved).
+// nsplit workgroups of tpw tiles, enough workgroups to fill the CUs.
 struct DnPlan {
     int64_t tpw, nsplit;
     size_t lds;
@@ -948,12 +989,11 @@ struct DnPlan {
 DnPlan plan_down(int64_t E, int64_t H, int64_t I, int cus) {
     const int G = static_cast<int>(I / 64);
     const int64_t te = H / 16;  // 16-column tiles per expert
-    const int64_t max_tiles = static_cast<int64_t>((kLdsDynMax - dn_lds_bytes(G, 0)) / (static_cast<size_t>(16) * G * 4));
-    int64_t nsplit = std::max<int64_t>((cus + E - 1) / E, (te + max_tiles - 1) / max_tiles);
+    int64_t nsplit = (cus + E - 1) / E;
     nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, te));
     const int64_t tpw = (te + nsplit - 1) / nsplit;
     nsplit = (te + tpw - 1) / tpw;
-    return DnPlan{tpw, nsplit, dn_lds_bytes(G, static_cast<int>(tpw * 16))};
+    return DnPlan{tpw, nsplit, dn_lds_bytes(G)};
 }
 
 int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, const void* dn_s,
@@ -965,7 +1005,7 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     if (H % 64 != 0 || I % 64 != 0 || I > 64 * kDnMaxG || H >= (1 << 24) || E >= (1 << 24)) return KSL_ERR_SHAPE;
     if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(out2) % 16 ||
         reinterpret_cast<uintptr_t>(dn_s) % 16 || reinterpret_cast<uintptr_t>(dn_z) % 16 ||
-        reinterpret_cast<uintptr_t>(out3) % 8)
+        reinterpret_cast<uintptr_t>(out3) % 16)
         return KSL_ERR_ALIGN;
     DnArgs A;
     A.out2 = static_cast<const f16*>(out2);
@@ -976,6 +1016,8 @@ int launch_down(const void* out2, const int32_t* offsets, const uint8_t* dn_q, c
     A.out3 = static_cast<f16*>(out3);
     A.H = static_cast<int>(H);
     A.I = static_cast<int>(I);
+    A.early = nrows >= E ? 1 : 0;
+    A.sz = layout == kDnTiled ? reinterpret_cast<const uint32_t*>(dn_q + E * H * (I / 2)) : nullptr;
     // large routings: the GEMM-form row-block kernel (128-row blocks)
     if (nrows > kRowBlockFrom) {
         if (!rb_down_fits(H, I)) return KSL_ERR_SHAPE;  // not reached within the contract above
@@ -1068,21 +1110,34 @@ extern "C" int ksl_moe_preshuffle_ns_down(const uint8_t* dn_q, int64_t E, int64_
     return KSL_OK;
 }
 
-extern "C" int ksl_moe_repack_down(const uint8_t* dn_q, int64_t E, int64_t H, int64_t I, uint8_t* dn_q_tiled,
-                                   void* stream) {
+extern "C" size_t ksl_moe_repack_down_bytes(int64_t E, int64_t H, int64_t I) {
+    if (E <= 0 || H <= 0 || I <= 0 || H % 16 != 0 || I % 64 != 0) return 0;
+    return static_cast<size_t>(E * H * (I / 2) + E * H * (I / 64) * 4);
+}
+
+extern "C" int ksl_moe_repack_down(const uint8_t* dn_q, const void* dn_s, const void* dn_z, int64_t E, int64_t H,
+                                   int64_t I, uint8_t* dn_q_tiled, void* stream) {
     using namespace ksl;
     if (E <= 0 || H <= 0 || I <= 0 || H % 16 != 0 || I % 64 != 0) return KSL_ERR_SHAPE;
-    if (!dn_q || !dn_q_tiled) return KSL_ERR_ARG;
+    if (!dn_q || !dn_s || !dn_z || !dn_q_tiled) return KSL_ERR_ARG;
     if (dn_q == dn_q_tiled) return KSL_ERR_ARG;  // out of place
-    if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(dn_q_tiled) % 16) return KSL_ERR_ALIGN;
+    if (reinterpret_cast<uintptr_t>(dn_q) % 16 || reinterpret_cast<uintptr_t>(dn_q_tiled) % 16 ||
+        reinterpret_cast<uintptr_t>(dn_s) % 2 || reinterpret_cast<uintptr_t>(dn_z) % 2)
+        return KSL_ERR_ALIGN;
     const int64_t ntiles = E * (H / 16);
     const int g2n = static_cast<int>(I / 128), tail = (I % 128) != 0;
     const int64_t n = ntiles * (g2n * kWave + (tail ? kWave : 0));
     const int64_t grid = (n + 255) / 256;
-    if (grid >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
-    hipLaunchKernelGGL(repack_down_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), dn_q, dn_q_tiled, ntiles, static_cast<int>(I / 2), g2n,
-                       tail);
+    const int G = static_cast<int>(I / 64);
+    const int64_t gridp = (ntiles * G * 16 + 255) / 256;
+    if (grid >= (int64_t(1) << 31) || gridp >= (int64_t(1) << 31)) return KSL_ERR_SHAPE;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(repack_down_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, st, dn_q, dn_q_tiled,
+                       ntiles, static_cast<int>(I / 2), g2n, tail);
+    KSL_LAUNCH_CHECK();
+    hipLaunchKernelGGL(pair_scales_kernel, dim3(static_cast<unsigned>(gridp)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(dn_s), static_cast<const uint16_t*>(dn_z), ntiles, G,
+                       reinterpret_cast<uint32_t*>(dn_q_tiled + E * H * (I / 2)));
     KSL_LAUNCH_CHECK();
     return KSL_OK;
 }

@@ -222,20 +222,43 @@ def _cache_put(cache: dict | None, key, value, *sources) -> None:
 
 
 def dn_layout(exp) -> int:
-    return _lib.DN_LAYOUT_TILED if getattr(exp, "dn_tiled", False) else _lib.DN_LAYOUT_REF
+    """The C ABI's down layout code of exp. A tiled module's dn_q must be the
+    front of a buffer written by ksl_moe_repack_down (the down kernel reads
+    the pair table behind it): checked here on the host, so that a copy of
+    the bare [E, H, I/2] view (which drops the table) is refused."""
+    if not getattr(exp, "dn_tiled", False):
+        return _lib.DN_LAYOUT_REF
+    q = exp.dn_q
+    E, H, Ih = q.shape
+    need = int(_lib.load().ksl_moe_repack_down_bytes(E, H, 2 * Ih))
+    st = q.untyped_storage()
+    have = st.nbytes() - (q.data_ptr() - st.data_ptr())
+    if have < need:
+        raise ValueError("exp.dn_q is flagged dn_tiled but holds no pair table behind its weights "
+                         "(a copy of the tiled view?): re-run enable_tiled_down on the reference layout")
+    return _lib.DN_LAYOUT_TILED
 
 
 @torch.no_grad()
-def tiled_down(dn_q: torch.Tensor) -> torch.Tensor:
-    """dn_q [E, H, I/2] uint8 (reference layout) -> a new tensor of the same
-    shape in the tiled layout (ksl_moe_repack_down)."""
+def tiled_down(dn_q: torch.Tensor, dn_s: torch.Tensor, dn_z: torch.Tensor) -> torch.Tensor:
+    """dn_q [E, H, I/2] uint8 (reference layout) with its scales and
+    zero-points fp16 [E, H, I/64] -> a new [E, H, I/2] tensor in the tiled
+    layout, the front of a buffer whose tail holds the (scale, zero) pair
+    table the down kernel streams (ksl_moe_repack_down)."""
     E, H, Ih = dn_q.shape
     if not dn_q.is_cuda or dn_q.dtype != torch.uint8 or not dn_q.is_contiguous():
         raise ValueError("dn_q must be a contiguous uint8 tensor on the GPU")
-    out = torch.empty_like(dn_q)
-    rc = _lib.load().ksl_moe_repack_down(_lib.ptr(dn_q), E, H, 2 * Ih, _lib.ptr(out), _lib.stream_of(dn_q))
+    for name, t in (("dn_s", dn_s), ("dn_z", dn_z)):
+        if t.dtype != torch.float16 or tuple(t.shape) != (E, H, 2 * Ih // 64) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float16 [E, H, I/64] tensor")
+        if t.device != dn_q.device:
+            raise ValueError(f"{name} is on {t.device}, dn_q on {dn_q.device}")
+    lib = _lib.load()
+    buf = torch.empty(int(lib.ksl_moe_repack_down_bytes(E, H, 2 * Ih)), dtype=torch.uint8, device=dn_q.device)
+    rc = lib.ksl_moe_repack_down(_lib.ptr(dn_q), _lib.ptr(dn_s), _lib.ptr(dn_z), E, H, 2 * Ih, _lib.ptr(buf),
+                                 _lib.stream_of(dn_q))
     _lib.check(rc, "ksl_moe_repack_down")
-    return out
+    return buf[: E * H * Ih].view(E, H, Ih)
 
 
 def enable_tiled_down(exp, cache: dict | None = None):
@@ -248,13 +271,13 @@ def enable_tiled_down(exp, cache: dict | None = None):
     experts of a layer, kernels/load_w4_checkpoint.py:56-59) keep sharing one."""
     if getattr(exp, "dn_tiled", False):
         return exp
-    src = exp.dn_q
-    key = (src.data_ptr(), str(src.device), bool(getattr(exp, "dn_ns", False)))
-    t = _cache_get(cache, key, src)
+    srcs = (exp.dn_q, exp.dn_s, exp.dn_z)
+    key = tuple(t.data_ptr() for t in srcs) + (str(exp.dn_q.device), bool(getattr(exp, "dn_ns", False)))
+    t = _cache_get(cache, key, *srcs)
     if t is None:
-        ref = unshuffle_ns_down(src) if getattr(exp, "dn_ns", False) else src
-        t = tiled_down(ref)
-        _cache_put(cache, key, t, src)
+        ref = unshuffle_ns_down(exp.dn_q) if getattr(exp, "dn_ns", False) else exp.dn_q
+        t = tiled_down(ref, exp.dn_s, exp.dn_z)
+        _cache_put(cache, key, t, *srcs)
     exp.dn_q = t
     exp.dn_ns = False
     exp.dn_tiled = True

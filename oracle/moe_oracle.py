@@ -142,6 +142,18 @@ def tile_down(dn_q: np.ndarray) -> np.ndarray:
     return np.concatenate([main, tail], axis=-1).reshape(E, H, Ih)
 
 
+def down_pair_table(dn_s: np.ndarray, dn_z: np.ndarray) -> np.ndarray:
+    """The (scale, zero) pair table the tiled layout carries behind its
+    weights (this build's load-time repack): per 16-row tile T, group g and
+    row col of the tile, uint32 (scale bits | zero bits << 16) at index
+    (T * G + g) * 16 + col, G = I / 64."""
+    E, H, G = dn_s.shape
+    sb = dn_s.astype(np.float16).view(np.uint16).astype(np.uint32)
+    zb = dn_z.astype(np.float16).view(np.uint16).astype(np.uint32)
+    pairs = (sb | (zb << 16)).reshape(E, H // 16, 16, G)
+    return np.ascontiguousarray(pairs.transpose(0, 1, 3, 2)).reshape(-1)
+
+
 def preshuffle_ns_down(dn_q: np.ndarray, bk: int = 64) -> np.ndarray:
     """The reference's MOE_NS down pack (kernels/fused_moe_w4_v2.py:187-197,
     preshuffle_T_dn): unpack [E, N, K/2] to codes, and within each bk-chunk

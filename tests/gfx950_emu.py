@@ -86,6 +86,7 @@ class Wave:
         if t == "m0": return self.m0
         if t == "scc": return self.scc
         if t in ("vcc_lo",): return self.vcc & M32
+        if t in ("vcc_hi",): return self.vcc >> 32
         r = self.sreg(t)
         if r is not None:
             for i in r:
@@ -93,6 +94,13 @@ class Wave:
             val = 0
             for k, i in enumerate(r): val |= self.s[i] << (32 * k)
             return val
+        m = re.match(r"([\w.$]+)@rel32@(lo|hi)[+-]\d+$", t)
+        if m:
+            # PC-relative address of a device symbol: s_getpc_b64 reads as 0,
+            # so the relocation halves are the symbol's own address (a buffer
+            # registered under its mangled name)
+            a = self.buffers[m.group(1)][0]
+            return a & M32 if m.group(2) == "lo" else a >> 32
         L = self.lit(t)
         if L is not None:
             if n == 2 and L < 0x100000000 and t.startswith("-"): return L
@@ -102,6 +110,8 @@ class Wave:
         if t == "vcc": self.vcc = val & 0xFFFFFFFFFFFFFFFF; return
         if t == "exec": self.exec = val & 0xFFFFFFFFFFFFFFFF; return
         if t == "m0": self.m0 = val & M32; return
+        if t == "vcc_lo": self.vcc = (self.vcc & ~M32) | (val & M32); return
+        if t == "vcc_hi": self.vcc = (self.vcc & M32) | ((val & M32) << 32); return
         r = self.sreg(t)
         for k, i in enumerate(r):
             self.s[i] = (val >> (32 * k)) & M32; self.sk[i] = known
@@ -222,7 +232,7 @@ def run(ins, labels, w, max_steps=2_000_000):
             continue
         # ---- vector memory
         if op.startswith("global_load_lds"):
-            addr, kn = w.vget(t[0], 2)
+            addr, kn = gaddr(w, t[0], t[1])
             if w.check_inflight_read(t[0]): w.errors.append(("POISONED ADDRESS lds_dma", w.cur))
             if getattr(w, "m0poison", False): w.errors.append(("POISONED M0", w.cur))
             w.check_addr(addr, kn, 16, "lds_dma", w.act())
@@ -234,8 +244,9 @@ def run(ins, labels, w, max_steps=2_000_000):
                     for b in range(16): w.lds.pop(lds + 16 * l + b, None)
             w.vmq.append([set(), set()]); continue
         if op.startswith("global_load"):
-            n = {"global_load_dword": 1, "global_load_dwordx2": 2, "global_load_dwordx4": 4}[op]
-            addr, kn = w.vget(t[1], 2)
+            n = {"global_load_dword": 1, "global_load_dwordx2": 2, "global_load_dwordx4": 4,
+                 "global_load_ushort": 1}[op]
+            addr, kn = gaddr(w, t[1], t[2])
             off = 0
             for x in t[3:]:
                 if x.startswith("offset:"): off = int(x[7:], 0)
@@ -258,6 +269,50 @@ def run(ins, labels, w, max_steps=2_000_000):
                     if i in q[0]: q[1].add(i)
                 w.poison[i] = False
             w.vmq.append([set(r), set()]); continue
+        if op.startswith("scratch_store") or op.startswith("scratch_load"):
+            # register spills: private per-lane memory, dword granular
+            store = op.startswith("scratch_store")
+            size = {"byte": 1, "short": 2, "dword": 4, "dwordx2": 8, "dwordx3": 12, "dwordx4": 16}[op.split("_", 2)[2]
+                                                                                                 .replace("ubyte", "byte").replace("ushort", "short").replace("sbyte", "byte").replace("sshort", "short")
+                                                                                                 .replace("short_d16_hi", "short").replace("short_d16", "short")]
+            data, vaddr, saddr = (t[1], t[0], t[2]) if store else (t[0], t[1], t[2])
+            off = 0
+            for x in t[3:]:
+                if x.startswith("offset:"): off = int(x[7:], 0)
+            base = np.zeros(NL, dtype=np.uint64); kb = np.ones(NL, dtype=bool)
+            if vaddr != "off": base, kb = w.vget(vaddr)
+            if saddr != "off": base = base + np.uint64(w.sget(saddr))
+            if not hasattr(w, "scratch"): w.scratch = {}
+            act = w.act()
+            nd = max(1, size // 4)
+            if store:
+                if w.check_inflight_read(data): w.errors.append(("STALE DATA spilled", w.cur))
+                vals, kn = w.vget(data, nd)
+                regs = w.vreg(data)
+                pz = any(w.poison[i] for i in regs)
+                for l in range(NL):
+                    if not act[l]: continue
+                    if not kb[l]: w.errors.append(("scratch unknown address", w.cur)); continue
+                    a = int(base[l]) + off
+                    for k in range(nd):
+                        v = int(w.v[regs[k]][l]) if k < len(regs) else 0
+                        w.scratch[(l, a + 4 * k)] = (v, bool(w.vk[regs[k]][l]) and size >= 4, pz)
+                w.vmq.append([set(), set()]); continue
+            r = w.vreg(data)
+            for k, i in enumerate(r):
+                vals = np.zeros(NL, dtype=np.uint64); kn = np.zeros(NL, dtype=bool); pz = False
+                for l in range(NL):
+                    if act[l] and kb[l]:
+                        e = w.scratch.get((l, int(base[l]) + off + 4 * k))
+                        if e is not None:
+                            vals[l], kn[l] = e[0], e[1] and size >= 4
+                            pz = pz or e[2]
+                w.v[i] = np.where(act, vals, w.v[i])
+                w.vk[i] = np.where(act, kn, w.vk[i])
+                for q in w.vmq:
+                    if i in q[0]: q[1].add(i)
+                w.poison[i] = pz
+            w.vmq.append([set(r), set()]); continue
         if op.startswith("buffer_store"):
             n = {"buffer_store_dword": 1, "buffer_store_dwordx2": 2, "buffer_store_dwordx4": 4}[op]
             if w.check_inflight_read(t[0]): w.errors.append(("STALE DATA stored", w.cur))
@@ -277,6 +332,52 @@ def run(ins, labels, w, max_steps=2_000_000):
             w.vmq.append([set(), set()]); continue
         if op.startswith("ds_") or op.startswith("v_mfma") or op.startswith("v_pk_") or op.startswith("v_cvt_pk_f16") \
                 or op in ("v_add_f16_e32", "v_and_or_b32") and False:
+            if op.startswith("ds_write2") or op.startswith("ds_read2"):
+                # two accesses of one element size (b32 / b64): offset0 / offset1
+                # in elements (x64 for the st64 forms)
+                es = 8 if op.endswith("b64") else 4
+                unit = es * (64 if "st64" in op else 1)
+                o0 = o1 = 0
+                for x in t:
+                    if x.startswith("offset0:"): o0 = int(x[8:], 0)
+                    if x.startswith("offset1:"): o1 = int(x[8:], 0)
+                write = op.startswith("ds_write2")
+                av = t[0] if write else t[1]
+                if w.check_inflight_read(av): w.errors.append(("POISONED ADDRESS ds", w.cur))
+                a, ka = w.vget(av); act = w.act()
+                if write:
+                    if any(w.check_inflight_read(x) for x in t[1:3]): w.errors.append(("STALE DATA to LDS", w.cur))
+                    for half, (dreg, oo) in enumerate(((t[1], o0), (t[2], o1))):
+                        regs = w.vreg(dreg)
+                        for l in range(NL):
+                            if not act[l]: continue
+                            if not ka[l]: w.errors.append(("ds_write unknown address", w.cur)); break
+                            base = int(a[l]) + oo * unit
+                            if base + es > w.lds_size: w.errors.append(("ds_write beyond LDS", base, w.cur))
+                            for b in range(es):
+                                i = regs[b // 4]
+                                w.lds[base + b] = ((int(w.v[i][l]) >> (8 * (b % 4))) & 0xFF, bool(w.vk[i][l]))
+                    continue
+                r = w.vreg(t[0]); nd = es // 4
+                for half, oo in enumerate((o0, o1)):
+                    for j in range(nd):
+                        i = r[half * nd + j]
+                        vals = np.zeros(NL, dtype=np.uint64); kn = np.zeros(NL, dtype=bool)
+                        for l in range(NL):
+                            if not act[l] or not ka[l]: continue
+                            base = int(a[l]) + oo * unit + 4 * j
+                            if base + 4 > w.lds_size: w.errors.append(("ds_read beyond LDS", base, w.cur))
+                            v = 0; k = True
+                            for b in range(4):
+                                e = w.lds.get(base + b)
+                                if e is None: k = False; break
+                                v |= e[0] << (8 * b); k &= e[1]
+                            vals[l] = v; kn[l] = k
+                        w.v[i] = np.where(act, vals, w.v[i]); w.vk[i] = np.where(act, kn, w.vk[i])
+                        for q in w.vmq:
+                            if i in q[0]: q[1].add(i)
+                        w.poison[i] = False
+                continue
             if op.startswith("ds_write"):
                 if w.check_inflight_read(t[0]): w.errors.append(("POISONED ADDRESS ds", w.cur))
                 if any(w.check_inflight_read(x) for x in t[1:]): w.errors.append(("STALE DATA to LDS", w.cur))
@@ -392,6 +493,8 @@ def sop(w, op, t):
     if op == "s_ashr_i64": w.sset(t[0], (signed64(g(t[1], 2)) >> (g(t[2]) & 63)) & 0xFFFFFFFFFFFFFFFF, 2); return
     if op == "s_and_b32": r = g(t[1]) & g(t[2]); w.sset(t[0], r); w.scc = int(r != 0); return
     if op == "s_or_b32": r = g(t[1]) | g(t[2]); w.sset(t[0], r); w.scc = int(r != 0); return
+    if op == "s_andn2_b32": r = g(t[1]) & ~g(t[2]) & M32; w.sset(t[0], r); w.scc = int(r != 0); return
+    if op == "s_orn2_b32": r = (g(t[1]) | ~g(t[2])) & M32; w.sset(t[0], r); w.scc = int(r != 0); return
     if op == "s_xor_b32": r = g(t[1]) ^ g(t[2]); w.sset(t[0], r); w.scc = int(r != 0); return
     if op == "s_not_b32": r = (~g(t[1])) & M32; w.sset(t[0], r); w.scc = int(r != 0); return
     if op == "s_and_b64": r = g(t[1], 2) & g(t[2], 2); w.sset(t[0], r, 2); w.scc = int(r != 0); return
@@ -405,6 +508,7 @@ def sop(w, op, t):
         old = w.exec; w.sset(t[0], old, 2); w.exec = g(t[1], 2) & ~old & 0xFFFFFFFFFFFFFFFF; w.scc = int(w.exec != 0); return
     if op == "s_or_saveexec_b64":
         old = w.exec; w.sset(t[0], old, 2); w.exec = g(t[1], 2) | old; w.scc = int(w.exec != 0); return
+    if op == "s_brev_b32": w.sset(t[0], int(f"{g(t[1]) & M32:032b}"[::-1], 2)); return
     if op == "s_abs_i32": r = abs(signed32(g(t[1]))) & M32; w.sset(t[0], r); w.scc = int(r != 0); return
     if op in ("s_min_i32", "s_max_i32"):
         a, b = signed32(g(t[1])), signed32(g(t[2])); r = min(a, b) if op == "s_min_i32" else max(a, b)
@@ -425,14 +529,27 @@ def sop(w, op, t):
     if op == "s_bfe_u32":
         v = g(t[2]); off, wd = v & 31, (v >> 16) & 127; w.sset(t[0], (g(t[1]) >> off) & ((1 << wd) - 1)); return
     if op == "s_getreg_b32": w.sset(t[0], 0); return
+    if op == "s_getpc_b64": w.sset(t[0], 0, 2); return
     raise NotImplementedError(op + " " + " ".join(t))
+
+def gaddr(w, vaddr, saddr):
+    """Per-lane address of a global memory instruction: a 64-bit vector
+    address (saddr "off"), or a scalar base plus a 32-bit vector offset."""
+    if saddr == "off":
+        return w.vget(vaddr, 2)
+    vo, kn = w.vget(vaddr)
+    try:
+        sb = w.sget(saddr, 2)
+    except Unknown:
+        return np.zeros(NL, dtype=np.uint64), np.zeros(NL, dtype=bool)
+    return np.array([(int(sb) + int(x)) & 0xFFFFFFFFFFFFFFFF for x in vo], dtype=np.uint64), kn
 
 def vop(w, op, t):
     U = np.uint64; MM = U(M32)
     g = lambda x, n=1: w.vget(x, n)
     act = w.act()
     def setv(val, kn, dst=None): w.vset(dst or t[0], val & U(0xFFFFFFFFFFFFFFFF), kn)
-    base = op.replace("_e32", "").replace("_e64", "")
+    base = op.replace("_e32", "").replace("_e64", "").replace("_sdwa", "")
     def s32(a): return np.where(a & U(0x80000000), a.astype(np.int64) - (1 << 32), a.astype(np.int64))
     if base in ("v_mov_b32",): a, k = g(t[1]); setv(a & MM, k); return
     if base == "v_mov_b64": a, k = g(t[1], 2); setv(a, k); return
@@ -456,6 +573,16 @@ def vop(w, op, t):
         for l in range(NL):
             if act[l] and c[l]: m |= 1 << l
         w.sset(cdst, m, 2); return
+    if base in ("v_addc_co_u32", "v_subb_co_u32"):
+        # dst, carry out, a, b, carry in
+        a, ka = g(t[2]); b, kb = g(t[3]); cin = w.sget(t[4], 2)
+        m = 0; out = []
+        for l in range(NL):
+            ci = (cin >> l) & 1
+            v = int(a[l]) + int(b[l]) + ci if base == "v_addc_co_u32" else int(a[l]) - int(b[l]) - ci
+            out.append(v & M32)
+            if act[l] and (v > M32 or v < 0): m |= 1 << l
+        setv(np.array(out, dtype=U), ka & kb); w.sset(t[1], m, 2); return
     if base == "v_lshl_add_u64":
         a, ka = g(t[1], 2); sh = int(t[2], 0) if t[2].isdigit() else None
         if sh is None: shv, ks = g(t[2]); sh = int(shv[0])
@@ -469,6 +596,10 @@ def vop(w, op, t):
         a, ka = g(t[2]); b, kb = g(t[3]); c, kc = g(t[4], 2)
         r = np.array([(signed32(int(x)) * signed32(int(y)) + signed64(int(z))) & 0xFFFFFFFFFFFFFFFF for x, y, z in zip(a, b, c)], dtype=U)
         setv(r, ka & kb & kc); w.sset(t[1], 0, 2); return
+    if base in ("v_lshlrev_b64", "v_lshrrev_b64"):
+        a, ka = g(t[1]); b, kb = g(t[2], 2); sh = a & U(63)
+        r = (b << sh) if base == "v_lshlrev_b64" else (b >> sh)
+        setv(r & U(0xFFFFFFFFFFFFFFFF), ka & kb); return
     if base in ("v_lshlrev_b32", "v_lshrrev_b32", "v_ashrrev_i32"):
         a, ka = g(t[1]); b, kb = g(t[2]); sh = a & U(31)
         if base == "v_lshlrev_b32": r = (b << sh) & MM

@@ -101,10 +101,13 @@ def test_validation_returns_before_device_work(L):
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, fake, 7, null) == 1   # unknown layout
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, -1, fake, 0, null) == 2
     assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, P((1 << 20) + 4), 0, null) == 3  # out3 % 8
+    assert L.ksl_moe_down(fake, fake, fake, fake, fake, 128, 2816, 704, 2048, P((1 << 20) + 8), 0, null) == 3  # out3 % 16
     # repack: shapes, in-place refused, alignment
-    assert L.ksl_moe_repack_down(fake, 128, 2816, 700, P((1 << 21)), null) == 2
-    assert L.ksl_moe_repack_down(fake, 128, 2816, 704, fake, null) == 1
-    assert L.ksl_moe_repack_down(P((1 << 20) + 8), 128, 2816, 704, P(1 << 21), null) == 3
+    assert L.ksl_moe_repack_down(fake, fake, fake, 128, 2816, 700, P((1 << 21)), null) == 2
+    assert L.ksl_moe_repack_down(fake, fake, fake, 128, 2816, 704, fake, null) == 1
+    assert L.ksl_moe_repack_down(P((1 << 20) + 8), fake, fake, 128, 2816, 704, P(1 << 21), null) == 3
+    assert L.ksl_moe_repack_down(fake, P((1 << 20) + 1), fake, 128, 2816, 704, P(1 << 21), null) == 3  # dn_s % 2
+    assert L.ksl_moe_repack_down_bytes(128, 2816, 704) == 128 * 2816 * 352 + 128 * 2816 * 11 * 4
     # align: E above the routing limit
     assert L.ksl_moe_align(fake, 4, 8, 4096, 32, fake, fake, fake, null) == 2
 
@@ -155,22 +158,21 @@ def test_block_tail_entry_points_reject_bad_arguments_without_launching():
     assert block(T=0) == 0
 
 
-def test_down_lds_sizing_leaves_room_for_static_lds(L):
-    """ksl_moe_down's column split keeps dynamic LDS + the kernel's 16 bytes
-    of static LDS (find_row_block's int[3]) within gfx950's 160 KB, over the
+def test_down_lds_sizing_fits_gfx950(L):
+    """ksl_moe_down's dynamic LDS: the activation blocks of one 64-row chunk
+    (4 M tiles x I/64 x 2 blocks of 1 KB) and each of the 8 waves' output
+    staging (2 M tiles x 16 rows x 80 bytes), within gfx950's 160 KB over the
     corners of the contract (E <= 512, H <= 4096, I <= 1024) and device sizes
-    from 1 to 1024 CUs, including the shapes where the split is limited by
-    LDS rather than by the CU count (E=128, H=4096, I=1024; E=256, H=3072, I=512)."""
-    static = 16
+    from 1 to 1024 CUs; the largest at I = 1024."""
     worst = 0
     for E in (1, 8, 128, 256, 512):
         for H in (128, 256, 2816, 3072, 4096):
             for I in (64, 128, 512, 704, 768, 1024):
                 for cus in (1, 80, 256, 304, 1024):
                     lds = L.ksl_moe_down_lds_bytes(E, H, I, cus)
-                    assert lds > 0, (E, H, I, cus)
-                    assert lds + static <= 160 * 1024, (E, H, I, cus, lds)
+                    assert lds == 4 * 2 * (I // 64) * 1024 + 8 * 2 * 16 * 80, (E, H, I, cus, lds)
+                    assert lds <= 160 * 1024, (E, H, I, cus, lds)
                     worst = max(worst, lds)
-    assert worst > 150 * 1024  # the LDS-limited shapes are among the cases
+    assert worst == 4 * 2 * 16 * 1024 + 8 * 2 * 16 * 80
     assert L.ksl_moe_down_lds_bytes(128, 4096, 1088, 256) == 0  # I above the contract
     assert L.ksl_moe_down_lds_bytes(128, 4096, 100, 256) == 0   # I % 64 != 0

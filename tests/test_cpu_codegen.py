@@ -1,19 +1,20 @@
 """The down kernel's generated code, checked on the CPU.
 
-ksl_moe_down streams each wave's weight tiles through two register buffers
-loaded by inline asm (the compiler's own waits would drain the prefetch), so
-correctness depends on the register allocator never copying or reusing a
-buffer register while its load is in flight. The device assembly of
-csrc/moe_gemm.hip is built with the library's flags and a few workgroups of
-down_kernel are run through tests/gfx950_emu.py: every global, buffer and LDS
-access must stay in its buffer and no address, stored value or MFMA operand
-may come from a register whose load had not landed. Shapes: the 256-token
-layer (one chunk, up to two M tiles), 1024 tokens (four M tiles, several
-chunks per expert), a Zipf routing of 1024 tokens (experts of a few to many
-chunks), and small / odd I (a 64-K tail group, the largest I). Above 8192
-routed rows a different kernel runs (moe_rbgemm.hip): ordinary register
-loads for its weights, and inline-asm LDS reads of its activation fragments,
-whose in-flight windows are checked below on the generated code."""
+ksl_moe_down streams each wave's weight tiles (with their scale / zero-point
+pairs) into registers by ordinary loads, whose waits the compiler places,
+reads its activations from LDS and sends its outputs through a per-wave LDS
+staging area. The device assembly of csrc/moe_gemm.hip is
+built with the library's flags and a few workgroups of down_kernel are run
+through tests/gfx950_emu.py: every global, buffer and LDS access must stay in
+its buffer (the weights, the tiled layout's trailing pair table, out2,
+out3), and no address, stored value or MFMA operand may come from a register
+whose load had not landed (the compiler's waits are checked, not assumed).
+Shapes: the 256-token layer (one chunk, up to two M tiles), 1024 tokens (four
+M tiles, several chunks per expert), a Zipf routing of 1024 tokens (experts of
+a few to many chunks), and small / odd I (a 64-K tail group, the largest I).
+Above 8192 routed rows a different kernel runs (moe_rbgemm.hip): ordinary
+register loads for its weights, and inline-asm LDS reads of its activation
+fragments, whose in-flight windows are checked below on the generated code."""
 from __future__ import annotations
 
 import importlib.util
@@ -55,19 +56,16 @@ def down_asm(tmp_path_factory):
 
 # The launch plan of csrc/moe_gemm.hip (plan_down, kDnWaves, kDnMaxMt)
 # restated for the emulated launches.
-NW, MAX_MT, LDS_DYN_MAX, CUS = 12, 4, 160 * 1024 - 64, 256
+NW, MAX_MT, CUS = 8, 4, 256
 
 
 def _plan(E, H, I):
     G = I // 64
     te = H // 16
-    base = MAX_MT * 2 * G * 1024
-    max_tiles = (LDS_DYN_MAX - base) // (16 * G * 4)
-    nsplit = max(-(-CUS // E), -(-te // max_tiles))
-    nsplit = max(1, min(nsplit, te))
+    nsplit = max(1, min(-(-CUS // E), te))
     tpw = -(-te // nsplit)
     nsplit = -(-te // tpw)
-    return nsplit, tpw, base + tpw * 16 * G * 4
+    return nsplit, tpw, MAX_MT * 2 * G * 1024 + NW * 2 * 16 * 80  # activations, then the waves' output staging
 
 
 def _routing(E, T, tk, kind, seed):
@@ -112,13 +110,17 @@ def test_down_kernel_addresses_and_register_flow(down_asm, E, H, I, T, tk, routi
 
     p_out2 = alloc("out2", nrows * I * 2)
     p_off = alloc("offsets", (E + 1) * 4)
-    p_q = alloc("dn_q", E * H * I // 2)
+    # the tiled layout's buffer: the weights, then the (scale, zero) pair table
+    p_q = alloc("dn_q", E * H * I // 2 + (E * H * G * 4 if layout == 1 else 0))
     p_s = alloc("dn_s", E * H * G * 2)
     p_z = alloc("dn_z", E * H * G * 2)
     p_out3 = alloc("out3", nrows * H * 2)
-    p_karg = alloc("kernarg", 256)
-    # DnArgs, then the first hidden argument (the grid's block count)
-    karg = struct.pack("<QQQQQQiiii", p_out2, p_off, p_q, p_s, p_z, p_out3, H, I, nsplit, tpw)
+    p_karg = alloc("kernarg", 352)
+    p_sz = p_q + E * H * I // 2 if layout == 1 else 0
+    early = 1 if nrows >= E else 0
+    # DnArgs (80 bytes), then the first hidden argument (the grid's block count)
+    karg = struct.pack("<QQQQQQQiiiii", p_out2, p_off, p_q, p_s, p_z, p_out3, p_sz, H, I, nsplit, tpw, early)
+    karg += b"\0" * (80 - len(karg))
     karg += struct.pack("<I", grid) + b"\0" * 60
     mem = {p_karg + k: struct.unpack("<I", karg[k:k + 4])[0] for k in range(0, len(karg), 4)}
     mem.update({p_off + 4 * e: int(offsets[e]) for e in range(E + 1)})

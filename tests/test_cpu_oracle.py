@@ -700,3 +700,22 @@ def test_combine_stock_known_answer():
     # skipped ids (>= E) contribute nothing
     got2 = mo.bf16_to_f32(mo.combine_stock(out3, np.arange(3), np.array([[3, 9, 0]], np.int64), w, 4, "bf16"))
     assert float(got2[0, 0]) == 256.0
+
+
+def test_down_pair_table_known_positions():
+    """The tiled layout's (scale, zero) pair table: row r = 16*T + col of
+    expert e, group g sits at index ((e*H/16 + T)*G + g)*16 + col, scale bits
+    low, zero bits high. Hand-checked entries: expert 1, row 35 (tile 2,
+    col 3), group 4 of G = 5, H = 64."""
+    E, H, G = 2, 64, 5
+    s = (np.arange(E * H * G, dtype=np.float32).reshape(E, H, G) / 1024).astype(np.float16)
+    z = (np.arange(E * H * G, dtype=np.float32).reshape(E, H, G) % 16).astype(np.float16)
+    t = mo.down_pair_table(s, z)
+    assert t.shape == (E * H * G,)
+    idx = ((1 * (H // 16) + 2) * G + 4) * 16 + 3
+    want = int(s[1, 35, 4].view(np.uint16)) | (int(z[1, 35, 4].view(np.uint16)) << 16)
+    assert int(t[idx]) == want
+    assert int(t[0]) == int(s[0, 0, 0].view(np.uint16)) | (int(z[0, 0, 0].view(np.uint16)) << 16)
+    # a permutation of the pairs: every (row, group) once
+    assert len(np.unique(t)) == len(np.unique((s.view(np.uint16).astype(np.uint32) |
+                                               (z.view(np.uint16).astype(np.uint32) << 16)).ravel()))

@@ -133,7 +133,7 @@ def test_block_forward_canvas_256(gpu):
     st = lib.stream_of(xd)
     bufs = [lib.ptr(getattr(exp, k)) for k in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z")]
     v2 = load_mod("fused_moe_w4_v2")
-    dn_t = v2.tiled_down(exp.dn_q)    # the block runs on the load-time repacked down weights
+    dn_t = v2.tiled_down(exp.dn_q, exp.dn_s, exp.dn_z)  # the block runs on the load-time repacked down weights
     bufs_t = bufs[:3] + [lib.ptr(dn_t)] + bufs[4:]
     print("block_forward T=256 H=2816 I=704 E=128 top-8", flush=True)
     rc = L.ksl_moe_layer_forward(lib.ptr(xd), lib.DTYPE_BF16, H, lib.ptr(pre_d), lib.DTYPE_BF16, 1e-6,

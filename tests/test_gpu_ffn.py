@@ -67,7 +67,7 @@ def _pack(gpu, exp, dn_layout):
                                     st), "ksl_moe_pack_gateup")
     dq = exp.dn_q
     if dn_layout == lib.DN_LAYOUT_TILED:
-        dq = load_mod("fused_moe_w4_v2").tiled_down(exp.dn_q)
+        dq = load_mod("fused_moe_w4_v2").tiled_down(exp.dn_q, exp.dn_s, exp.dn_z)
     lib.check(L.ksl_moe_pack_down(lib.ptr(dq), lib.ptr(exp.dn_s), lib.ptr(exp.dn_z), dn_layout, E, H, I,
                                   lib.ptr(dn), st), "ksl_moe_pack_down")
     return gu, dn

@@ -485,9 +485,16 @@ def test_repack_down_bit_exact(gpu, E, H, I):
     v2 = load_mod("fused_moe_w4_v2")
     g = torch.Generator().manual_seed(E + H + I)
     q = torch.randint(0, 256, (E, H, I // 2), generator=g, dtype=torch.uint8)
-    t = v2.tiled_down(q.to(gpu))
+    s = (0.005 + 0.015 * torch.rand(E, H, I // 64, generator=g)).to(torch.float16)
+    z = torch.randint(0, 16, (E, H, I // 64), generator=g).to(torch.float16)
+    t = v2.tiled_down(q.to(gpu), s.to(gpu), z.to(gpu))
     torch.cuda.synchronize()
     assert np.array_equal(_np(t), mo.tile_down(q.numpy()))
+    # the (scale, zero) pair table behind the weights
+    n = E * H * I // 2
+    table = t.untyped_storage()[n:n + E * H * (I // 64) * 4]
+    got = np.frombuffer(bytes(table.cpu()), dtype=np.uint32)
+    assert np.array_equal(got, mo.down_pair_table(s.numpy(), z.numpy()))
 
 
 @pytest.mark.parametrize("T,tk,E,H,I,seed", [(256, 8, 128, 2816, 704, 81), (40, 4, 16, 512, 256, 82)])
@@ -583,7 +590,7 @@ def test_down_row_blocks_bit_equal_to_expert_mode(gpu, E, H, I, T, zipf, layout)
     nrows = T * tk
     assert nrows > 8192
     exp = wl.make_experts(E, H, I, E + I + 1, device=gpu)
-    dn_q = v2.tiled_down(exp.dn_q) if layout == "tiled" else exp.dn_q
+    dn_q = v2.tiled_down(exp.dn_q, exp.dn_s, exp.dn_z) if layout == "tiled" else exp.dn_q
     code = lib.DN_LAYOUT_TILED if layout == "tiled" else lib.DN_LAYOUT_REF
     g = torch.Generator().manual_seed(E + I + 2)
     out2 = (0.5 * torch.randn(nrows, I, generator=g)).to(torch.float16).to(gpu)
