@@ -55,14 +55,41 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+def _check_generated_code(verbose: bool) -> None:
+    """The row-block GEMMs' inline-asm LDS reads rely on the compiler leaving
+    their destination registers alone until the wait that retires them: check
+    that on this build's assembly (codegen_check.py) and refuse to link a
+    library that breaks it."""
+    import tempfile
+    sys.path.insert(0, PKG_DIR)
+    try:
+        import codegen_check
+    finally:
+        sys.path.pop(0)
+    src = os.path.join(CSRC, "moe_rbgemm.hip")
+    with tempfile.TemporaryDirectory() as td:
+        out = os.path.join(td, "moe_rbgemm.s")
+        cmd = [HIPCC, *HIP_FLAGS, "-w", "--cuda-device-only", "-S", src, "-o", out]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc -S failed on moe_rbgemm.hip ({res.returncode}):\n{res.stderr[-8000:]}")
+        errs = codegen_check.check_rb_gemm(open(out).read())
+    if errs:
+        raise RuntimeError("generated-code check failed (moe_rbgemm.hip):\n" + "\n".join(errs))
+
+
 def build(verbose: bool = False) -> str:
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     os.makedirs(OBJ_DIR, exist_ok=True)
     workers = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), os.cpu_count() or 1))
-    with ThreadPoolExecutor(max_workers=workers) as pool:
+    with ThreadPoolExecutor(max_workers=workers + 1) as pool:
+        check = pool.submit(_check_generated_code, verbose)
         objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
+        check.result()
     tmp = LIB_PATH + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:

@@ -185,45 +185,16 @@ def rb_asm(tmp_path_factory):
     return out
 
 
-def _vregs(tok):
-    import re
-    m = re.match(r"v\[(\d+):(\d+)\]", tok)
-    if m:
-        return set(range(int(m.group(1)), int(m.group(2)) + 1))
-    m = re.match(r"v(\d+)$", tok)
-    return {int(m.group(1))} if m else set()
+def _codegen_check():
+    spec = importlib.util.spec_from_file_location(
+        "ksl_codegen_check", os.path.join(ROOT, "knivesysl-diffusion-xe_amd", "codegen_check.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
 def _ahead_windows(lines):
-    """For every `ds_read_b128 ...; ksl-ahead` (an LDS read issued by inline asm
-    whose result the compiler believes present at once), the instructions up to
-    the next s_waitcnt that retires it. Returns (reads, violations): a
-    violation is an instruction in the window that reads or writes one of the
-    destination registers, or a branch or label inside the window."""
-    reads, bad = 0, []
-    for i, line in enumerate(lines):
-        if "ksl-ahead" not in line or "ds_read_b128" not in line:
-            continue
-        reads += 1
-        dst = _vregs(line.split()[1].rstrip(","))
-        assert len(dst) == 4, line
-        for j in range(i + 1, len(lines)):
-            s = lines[j].split(";")[0].strip()
-            if not s:
-                continue
-            if s.startswith("s_waitcnt") and "lgkmcnt(0)" in s:
-                break
-            if s.endswith(":") or s.startswith("s_cbranch") or s.startswith("s_branch") or s.startswith("s_setpc"):
-                bad.append((i, s))
-                break
-            used = set()
-            for t in s.split()[1:]:
-                used |= _vregs(t.strip(","))
-            if used & dst:
-                bad.append((i, s))
-        else:
-            bad.append((i, "no wait before the function ends"))
-    return reads, bad
+    return _codegen_check().ahead_windows(lines)
 
 
 def test_rb_gemm_ahead_reads_stay_untouched_in_flight(rb_asm):
@@ -232,21 +203,16 @@ def test_rb_gemm_ahead_reads_stay_untouched_in_flight(rb_asm):
     fragment keeps its four destination registers untouched, with no branch,
     until the s_waitcnt lgkmcnt(0) that retires it; seven such reads per
     128-K step of the full-block path."""
-    text = open(rb_asm).read().split("\n")
-    fns = [l.split(":")[0] for l in text if l.startswith("_ZN3ksl12_GLOBAL__N_114rb_gemm_kernel")
-           and l.split(";")[0].strip().endswith(":")]
+    cc = _codegen_check()
+    asm = open(rb_asm).read()
+    fns = cc.rb_gemm_functions(asm)
     assert len(fns) == 4
-    for fn in fns:
-        i0 = next(i for i, l in enumerate(text) if l.startswith(fn + ":"))
-        ins = []
-        for l in text[i0 + 1:]:
-            if l.startswith(".Lfunc_end"):
-                break
-            ins.append(l.strip())
-        reads, bad = _ahead_windows(ins)
+    for fn, ins in fns.items():
+        reads, bad = cc.ahead_windows(ins)
         # gate/up: 4 steps of 7; down: 4 + 2 (the 64-K tail) steps of 7
         assert reads in (28, 42), (fn, reads)
         assert not bad, (fn, bad[:5])
+    assert cc.check_rb_gemm(asm) == []  # what build.py runs before it links
 
 
 def test_ahead_window_check_flags_a_touched_register():
