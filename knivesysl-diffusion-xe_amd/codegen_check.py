@@ -73,16 +73,17 @@ def rb_gemm_functions(asm_text: str) -> dict[str, list[str]]:
 
 def check_rb_gemm(asm_text: str) -> list[str]:
     """Violations of the ahead-read windows over every rb_gemm_kernel instance
-    (gate/up: 4 steps x 7 reads per 128-K group; down: 4 + 2 steps x 7), as
-    messages; empty when the code is sound."""
+    (7 reads per 32-K step: gate/up 4 steps per 128-K group, down 4 + 2 for
+    its 64-K tail, times however many copies of the loop body the compiler
+    emits), as messages; empty when the code is sound."""
     errs = []
     fns = rb_gemm_functions(asm_text)
     if len(fns) != 4:
         errs.append(f"expected 4 rb_gemm_kernel instances, found {len(fns)}")
     for fn, ins in fns.items():
         reads, bad = ahead_windows(ins)
-        if reads not in (28, 42):
-            errs.append(f"{fn}: {reads} ahead reads (expected 28 or 42)")
+        if reads == 0 or reads % 7:
+            errs.append(f"{fn}: {reads} ahead reads (expected a positive multiple of 7)")
         for b in bad[:5]:
             errs.append(f"{fn}: in-flight register or branch in an ahead-read window: {b}")
     return errs

@@ -126,13 +126,43 @@ def _check_act(exp) -> bool:
     return True
 
 
+class _WeakValueCache(dict):
+    """A cache for enable_tiled_down whose entries hold the converted tensor
+    weakly: an entry lives as long as some module still uses the tensor (its
+    sources are checked by identity, as in any cache given to it)."""
+
+    def get(self, key, default=None):
+        entry = super().get(key)
+        if entry is None:
+            return default
+        refs, vref = entry
+        value = vref()
+        if value is None:
+            del self[key]
+            return default
+        return refs, value
+
+    def __setitem__(self, key, entry):
+        refs, value = entry
+        super().__setitem__(key, (refs, weakref.ref(value)))
+
+
+# Modules still in the MOE_NS down layout at their first forward (no load-time
+# repack ran) are converted there, through this process-wide cache, so the
+# encoder and decoder experts of a layer that share one dn_q
+# (kernels/load_w4_checkpoint.py:56-59) keep sharing one converted tensor.
+_NS_FIRST_FORWARD = _WeakValueCache()
+
+
 def _check_weights(exp, E, H, I) -> None:
     """Shapes, dtypes, contiguity and device of the six buffers (host-side
-    only, no sync); a module in the MOE_NS down layout is converted first."""
+    only, no sync); a module in the MOE_NS down layout is converted first (one
+    allocation and one repack launch, once per shared buffer; repack_experts
+    or enable_ns_down at load time avoids that inside the first forward)."""
     if getattr(exp, "_ksl_weights_checked", False):
         return
     if getattr(exp, "dn_ns", False):
-        enable_tiled_down(exp)
+        enable_tiled_down(exp, _NS_FIRST_FORWARD)
     spec = {
         "gu_q": ((E, 2 * I, H // 2), torch.uint8),
         "gu_s": ((E, 2 * I, H // 128), torch.float16),

@@ -49,6 +49,34 @@ def test_ns_module_gives_the_plain_pack_output(gpu):
     assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
 
 
+def test_ns_modules_sharing_a_buffer_share_the_converted_one(gpu):
+    """Encoder and decoder experts of a layer share their buffers
+    (kernels/load_w4_checkpoint.py:56-59). Two modules flagged dn_ns over one
+    dn_q, converted at their first forwards (no load-time repack ran), end up
+    on one converted tensor, with the plain pack's output bits."""
+    wl = load_mod("workloads")
+    v2 = load_mod("fused_moe_w4_v2")
+    T, tk, E, H, I = 32, 8, 16, 256, 704
+    plain = wl.make_experts(E, H, I, 61).to(gpu)
+    enc = wl.make_experts(E, H, I, 61).to(gpu)
+    enc.dn_q = torch.from_numpy(mo.preshuffle_ns_down(enc.dn_q.cpu().numpy())).to(gpu)
+    enc.dn_ns = True
+    dec = wl.make_experts(E, H, I, 61).to(gpu)
+    for name in ("gu_q", "gu_s", "gu_z", "dn_q", "dn_s", "dn_z"):
+        setattr(dec, name, getattr(enc, name))
+    dec.dn_ns = True
+    hidden = wl.make_hidden(T, H, 62).to(gpu)
+    ids, w = wl.make_routing(T, E, tk, 63)
+    ids, w = ids.to(gpu), w.to(gpu)
+    y0 = v2.fused_moe_w4_v2(hidden, plain, ids, w)
+    y1 = v2.fused_moe_w4_v2(hidden, enc, ids, w)
+    y2 = v2.fused_moe_w4_v2(hidden, dec, ids, w)
+    torch.cuda.synchronize()
+    assert enc.dn_q is dec.dn_q and enc.dn_tiled and dec.dn_tiled
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(y0.view(torch.int16), y2.view(torch.int16))
+
+
 def test_zero_points_are_checked_at_load_time(gpu):
     wl = load_mod("workloads")
     v2 = load_mod("fused_moe_w4_v2")
