@@ -550,6 +550,8 @@ inline size_t dn_lds_bytes(int G) { return dn_act_bytes(G) + static_cast<size_t>
 template <int G2, bool TAIL, int LAYOUT>
 struct DnTile {
     static constexpr int NG = G2 + (TAIL ? 1 : 0);
+    // load instructions of one tile (dn_fetch)
+    static constexpr int kLoads = G2 + (TAIL ? 1 : 0) + (LAYOUT == kDnTiled ? NG : 2 * NG);
     u32x4 q[G2];
     u32x2 t[TAIL ? 1 : 0];
     uint32_t sz[LAYOUT == kDnTiled ? NG : 0];
@@ -767,27 +769,28 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
         dn_fetch<G2, TAIL, LAYOUT>(x0, A, row0 + 32 * p, ln);
         dn_fetch<G2, TAIL, LAYOUT>(x1, A, row0 + 16 * t1i, ln);
     };
-    // most experts have rows: the first pair's weights go out before the
-    // routing is read
-    const bool early = A.early && npw > 0;
-    if (early) fetch(0);
     const int start = A.offsets[e];
     const int M = A.offsets[e + 1] - start;
-    if (M <= 0) {
-        vm_wait<0>();  // early loads land before the wave ends
-        return;
-    }
+    if (M <= 0) return;
     for (int m0 = 0; m0 < M; m0 += 16 * MTX) {
         const int mrows = M - m0 < 16 * MTX ? M - m0 : 16 * MTX;
         const int mt = (mrows + 15) >> 4;
         if (m0 > 0) __syncthreads();  // every wave is done with the previous chunk's activations
         dn_stage_a<G2, TAIL>(A, lds, start, m0, mrows, mt, wave, rr, ch);
-        vm_wait<0>();
+        // the first pair's weights go out behind the activations; the barrier
+        // waits for the activations only (each wave's loads retire in order),
+        // so a wave starts once its own pair has landed, not the slowest one's
+        if (npw > 0) {
+            fetch(0);
+            vm_wait<2 * Tile::kLoads>();
+        } else {
+            vm_wait<0>();
+        }
         dma_barrier();
         const __amdgpu_buffer_rsrc_t out =
             raw_rsrc(A.out3 + static_cast<int64_t>(start + m0) * A.H, static_cast<uint32_t>(mrows * A.H * 2));
         for (int k = 0; k < npw; ++k) {
-            if (k > 0 || !(m0 == 0 && early)) fetch(k);
+            if (k > 0) fetch(k);
             const int p = wave + k * kDnWaves;
             // two straight-line passes, not a loop (a loop kept both tiles'
             // weights and every pass temporary live at once: spills)
