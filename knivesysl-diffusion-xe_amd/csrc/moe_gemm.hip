@@ -26,8 +26,9 @@
 //   - gate/up: producer waves stream weight and activation fragments of one
 //     128-K group per slot into an LDS ring by direct global -> LDS loads,
 //     consumer waves only read LDS (one barrier per group);
-//   - down: each wave streams its 16-column weight tiles through two register
-//     buffers with explicit vmcnt waits.
+//   - down: each wave loads a pair of 16-column weight tiles (with their
+//     scale / zero-point pair words) straight into registers by ordinary,
+//     compiler-tracked loads, and other waves of the SIMD cover the latency.
 //
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
@@ -489,12 +490,14 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
 // chunk) are copied into LDS once per chunk (direct global->LDS loads). Every
 // wave then walks pairs of 16-column tiles (pairs w, w + kDnWaves, ...): each
 // lane loads its weight words and the scale / zero-point of its groups for
-// both tiles of the next pair straight into registers, by ordinary loads that
-// the compiler tracks and waits for, while the current pair is decoded and
-// multiplied. The two tiles of a pair share every activation fragment read
-// from LDS (half the LDS reads of one tile at a time). Nothing is staged
-// before a wave's first pair but the activations, and no load is issued past
-// a wave's last pair (each weight byte is fetched once).
+// both tiles of the pair straight into registers, by ordinary loads that the
+// compiler tracks and waits for, then decodes and multiplies them; while one
+// wave waits for its pair the other wave of its SIMD computes (a second
+// register buffer per wave, measured, was not faster). The two tiles of a
+// pair share every activation fragment read from LDS (half the LDS reads of
+// one tile at a time). Nothing is staged before a wave's first pair but the
+// activations, and no load is issued past a wave's last pair (each weight
+// byte is fetched once).
 //
 // K mapping: one 16-byte load per lane and 128-K block, lane (col, c) holding
 // row col, nibbles 32c .. 32c+31 of the block: MFMA step i takes nibbles
