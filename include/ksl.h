@@ -239,8 +239,9 @@ int ksl_moe_act_to_down_order(const void* src, int64_t rows, int64_t I, void* ds
 
 /* Dynamic LDS bytes a ksl_moe_down launch requests for an (E, H, I) layer on
  * a device with cus compute units (host-only arithmetic, no device call; 0
- * for a shape outside the contract). Each workgroup also holds 16 bytes of
- * static LDS; the two together stay within gfx950's 160 KB per workgroup. */
+ * for a shape outside the contract): the activation blocks of one 64-row
+ * chunk (4 x I/64 x 2 KB) and each of the 8 waves' output staging (2.5 KB),
+ * at most 148 KB (I = 1024), within gfx950's 160 KB per workgroup. */
 size_t ksl_moe_down_lds_bytes(int64_t E, int64_t H, int64_t I, int64_t cus);
 
 /* Asymmetric group-wise 4-bit quantisation (load time): quantize_w4

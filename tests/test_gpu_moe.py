@@ -608,9 +608,9 @@ def test_down_row_blocks_bit_equal_to_expert_mode(gpu, E, H, I, T, zipf, layout)
 
 @pytest.mark.parametrize("E,H,I", [(128, 4096, 1024), (256, 3072, 512)])
 def test_down_at_lds_limited_shapes(gpu, E, H, I):
-    """The down launch at the contract's shapes whose column split is limited
-    by LDS (not by the CU count): it launches (dynamic + static LDS fit) and
-    matches the oracle on rows of 8 experts."""
+    """The down launch at the contract's largest shapes (I = 1024: the
+    largest LDS request; H = 4096; 256 experts): it launches and matches the
+    oracle on rows of 8 experts."""
     lib = load_pkg()._lib
     L = lib.load()
     g = torch.Generator().manual_seed(E + H + I)
