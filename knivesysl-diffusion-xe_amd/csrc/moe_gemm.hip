@@ -637,19 +637,17 @@ __device__ __forceinline__ void dn_fetch(DnTile<G2, TAIL, LAYOUT>& w, const DnAr
 }
 
 // Both tiles of a pair against two M tiles of activations: every activation
-// fragment read from LDS feeds one MFMA of each tile. (A chunk with an odd
-// number of M tiles computes one tile more than it has: its LDS blocks hold
-// other rows, and its outputs are dropped at the store. The launch time is
-// that of the workgroups whose experts have two M tiles, so the spare MFMAs of
-// one-tile experts cost no time.)
-template <int G2, bool TAIL, int LAYOUT>
+// fragment read from LDS feeds one MFMA of each tile. NT M tiles (1 or 2) per
+// pass: a chunk of three M tiles computes one more in its second pass (its LDS
+// blocks hold other rows; its outputs are dropped at the store).
+template <int G2, bool TAIL, int LAYOUT, int NT>
 __device__ __forceinline__ void dn_pair_mma(const DnTile<G2, TAIL, LAYOUT>& w0, const DnTile<G2, TAIL, LAYOUT>& w1,
-                                            f32x4 (&acc0)[2], f32x4 (&acc1)[2], const char* __restrict__ a_lds,
+                                            f32x4 (&acc0)[NT], f32x4 (&acc1)[NT], const char* __restrict__ a_lds,
                                             int fo, const NibConsts& kn) {
     constexpr int G = 2 * G2 + (TAIL ? 1 : 0);
     auto step = [&](const f16x8& b0, const f16x8& b1, int blk) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < NT; ++t) {
             const f16x8 a = *reinterpret_cast<const f16x8*>(a_lds + (t * 2 * G + blk) * kBlk + fo);
             acc0[t] = mfma16x16x32(b0, a, acc0[t]);
             acc1[t] = mfma16x16x32(b1, a, acc1[t]);
@@ -681,7 +679,7 @@ __device__ __forceinline__ void dn_pair_mma(const DnTile<G2, TAIL, LAYOUT>& w0, 
     }
 }
 
-// A pair's outputs for two M tiles. The weights are the MFMA's A operand and
+// A pair's outputs for NT M tiles. The weights are the MFMA's A operand and
 // the activations its B operand, so each accumulator is its tile transposed:
 // lane (col, c) holds row col of the M tile, the tile's output columns 4c ..
 // 4c+3. They go through the wave's LDS staging area (row-major, the pair's 32
@@ -689,12 +687,13 @@ __device__ __forceinline__ void dn_pair_mma(const DnTile<G2, TAIL, LAYOUT>& w0, 
 // contiguous bytes per row and one store per M tile. Rows past the chunk, or
 // a second tile past the workgroup's last, take an out-of-range offset
 // (dropped by the buffer store).
-__device__ __forceinline__ void dn_store_pair(const f32x4 (&acc0)[2], const f32x4 (&acc1)[2], char* o_lds,
+template <int NT>
+__device__ __forceinline__ void dn_store_pair(const f32x4 (&acc0)[NT], const f32x4 (&acc1)[NT], char* o_lds,
                                               __amdgpu_buffer_rsrc_t out, int H, int colw, bool second, int mrows,
                                               int lane, int row0) {
     const int col = lane & 15, c = lane >> 4;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NT; ++t) {
         const f16x4 v0{static_cast<f16>(acc0[t][0]), static_cast<f16>(acc0[t][1]), static_cast<f16>(acc0[t][2]),
                        static_cast<f16>(acc0[t][3])};
         const f16x4 v1{static_cast<f16>(acc1[t][0]), static_cast<f16>(acc1[t][1]), static_cast<f16>(acc1[t][2]),
@@ -706,7 +705,7 @@ __device__ __forceinline__ void dn_store_pair(const f32x4 (&acc0)[2], const f32x
     // lane (r = lane / 4, part = lane % 4): 16 bytes of row r, columns 8 * part ..
     const int r = lane >> 2, part = lane & 3;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NT; ++t) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(o_lds + (t * 16 + r) * kDnOutRow + part * 16);
         const int row = t * 16 + r;  // row0 + row of the chunk; mrows counted from row0
         const bool ok = row < mrows && (second || part < 2);
@@ -797,19 +796,24 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
             const int p = wave + k * kDnWaves;
             // two straight-line passes, not a loop (a loop kept both tiles'
             // weights and every pass temporary live at once: spills)
-            auto pass = [&](int t0) {
-                f32x4 acc0[2], acc1[2];
+            auto pass = [&](auto nt_c, int t0) {
+                constexpr int NT = decltype(nt_c)::value;
+                f32x4 acc0[NT], acc1[NT];
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
+                for (int t = 0; t < NT; ++t) {
                     acc0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                     acc1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                 }
-                dn_pair_mma<G2, TAIL, LAYOUT>(x0, x1, acc0, acc1, lds + t0 * 2 * G * kBlk, fo, kn);
-                dn_store_pair(acc0, acc1, o_lds, out, A.H, col0 + 32 * p, 2 * p + 1 < ntiles, mrows - 16 * t0, lane,
-                              t0 * 16);
+                dn_pair_mma<G2, TAIL, LAYOUT, NT>(x0, x1, acc0, acc1, lds + t0 * 2 * G * kBlk, fo, kn);
+                dn_store_pair<NT>(acc0, acc1, o_lds, out, A.H, col0 + 32 * p, 2 * p + 1 < ntiles, mrows - 16 * t0,
+                                  lane, t0 * 16);
             };
-            pass(0);
-            if (mt > 2) pass(2);
+            if (mt == 1) {
+                pass(std::integral_constant<int, 1>{}, 0);  // one M tile: half the MFMAs and LDS reads
+            } else {
+                pass(std::integral_constant<int, 2>{}, 0);
+                if (mt > 2) pass(std::integral_constant<int, 2>{}, 2);
+            }
         }
     }
 }
