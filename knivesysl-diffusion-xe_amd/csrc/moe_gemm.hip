@@ -638,8 +638,7 @@ __device__ __forceinline__ void dn_fetch(DnTile<G2, TAIL, LAYOUT>& w, const DnAr
 
 // Both tiles of a pair against two M tiles of activations: every activation
 // fragment read from LDS feeds one MFMA of each tile. NT M tiles (1 or 2) per
-// pass: a chunk of three M tiles computes one more in its second pass (its LDS
-// blocks hold other rows; its outputs are dropped at the store).
+// pass.
 template <int G2, bool TAIL, int LAYOUT, int NT>
 __device__ __forceinline__ void dn_pair_mma(const DnTile<G2, TAIL, LAYOUT>& w0, const DnTile<G2, TAIL, LAYOUT>& w1,
                                             f32x4 (&acc0)[NT], f32x4 (&acc1)[NT], const char* __restrict__ a_lds,
@@ -808,11 +807,14 @@ __global__ __launch_bounds__(kDnThreads) void down_kernel(DnArgs A) {
                 dn_store_pair<NT>(acc0, acc1, o_lds, out, A.H, col0 + 32 * p, 2 * p + 1 < ntiles, mrows - 16 * t0,
                                   lane, t0 * 16);
             };
+            // an odd last M tile goes in a one-tile pass (half the MFMAs and
+            // LDS reads of a two-tile pass)
             if (mt == 1) {
-                pass(std::integral_constant<int, 1>{}, 0);  // one M tile: half the MFMAs and LDS reads
+                pass(std::integral_constant<int, 1>{}, 0);
             } else {
                 pass(std::integral_constant<int, 2>{}, 0);
-                if (mt > 2) pass(std::integral_constant<int, 2>{}, 2);
+                if (mt == 3) pass(std::integral_constant<int, 1>{}, 2);
+                if (mt == 4) pass(std::integral_constant<int, 2>{}, 2);
             }
         }
     }
