@@ -60,6 +60,16 @@ namespace {
 
 constexpr int kRowBlockFrom = 8192;  // routed rows above which the row-block kernels run
 
+// Compile-time loop: f(integral_constant<int, 0>) .. f(integral_constant<int, N-1>).
+template <int N, typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
 // ---------------------------------------------------------------- gate / up
 // One workgroup covers NC*16 columns of I of one expert (NC = 11: 176 columns,
 // a quarter of DiffusionGemma's I = 704) with NC consumer waves and NP
@@ -266,73 +276,69 @@ __device__ __forceinline__ void gateup_produce_1w(const GuArgs& A, int e, int c0
     }
 }
 
-// Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
-template <int ACT, int NC, int NP, int R, int MT>
-__device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
-                                               const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
-    using S = GuShape<NC, NP, R>;
+// One quantisation group g of a consumer wave: its gate and up weight words in
+// slot sp, decoded against their zero-points, times the MT activation tiles
+// of the slot; the fp32 group partials are scaled into acc. sz: the
+// [s_gate | z_gate | s_up | z_up] table of the workgroup's rows, kCols x G each.
+template <int NC, int MT>
+__device__ __forceinline__ void gateup_group(const char* __restrict__ sp, const f16* __restrict__ sz, int G, int g,
+                                             const NibConsts& kn, f32x4 (&acc)[2][MT]) {
+    constexpr int kSlotW = 2 * NC * kBlk;
+    constexpr int kc = 16 * NC;
     const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int col = lane & 15, c = lane >> 4;
-    const int G = A.H >> 7;
-    const NibConsts kn = nib_consts();
-    const int kc = S::kCols;
-    const f16* s_g = lds_sz;
-    const f16* z_g = lds_sz + kc * G;
-    const f16* s_u = lds_sz + 2 * kc * G;
-    const f16* z_u = lds_sz + 3 * kc * G;
+    const f16* s_g = sz;
+    const f16* z_g = sz + kc * G;
+    const f16* s_u = sz + 2 * kc * G;
+    const f16* z_u = sz + 3 * kc * G;
     const int r = wave * 16 + col;  // row of the tile within the workgroup
     const int fo = frag_pos(col, c) * 16;
-    f32x4 acc[2][MT];
+    f32x4 part[2][MT];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();  // group 0 and the scale table are ready
-    int slot = 0;
-    for (int g = 0; g < G; ++g) {
-        const char* sp = lds + slot * S::kSlot;
-        f32x4 part[2][MT];
+        for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 wv[2];
+    ZeroPair zc[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) part[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        u32x4 wv[2];
-        ZeroPair zc[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            wv[j] = *reinterpret_cast<const u32x4*>(sp + (wave * 2 + j) * kBlk + fo);
-            zc[j] = zero_pair((j ? z_u : z_g)[r * G + g]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f16x8 a[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                a[t] = *reinterpret_cast<const f16x8*>(sp + S::kSlotW + (t * 4 + i) * kBlk + fo);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
-#pragma unroll
-                for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
-        }
-        slot = slot + 1 == R ? 0 : slot + 1;
-        __syncthreads();
+    for (int j = 0; j < 2; ++j) {
+        wv[j] = *reinterpret_cast<const u32x4*>(sp + (wave * 2 + j) * kBlk + fo);
+        zc[j] = zero_pair((j ? z_u : z_g)[r * G + g]);
     }
-    // epilogue: column c0 + wave*16 + col, gate tile 0 with up tile 1
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f16x8 a[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[t] = *reinterpret_cast<const f16x8*>(sp + kSlotW + (t * 4 + i) * kBlk + fo);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f16x8 b = nib8_minus_zero(wv[j][i], zc[j], kn);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) part[j][t] = mfma16x16x32(a[t], b, part[j][t]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float sc = static_cast<float>((j ? s_u : s_g)[r * G + g]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[j][t][q] = __builtin_fmaf(sc, part[j][t][q], acc[j][t][q]);
+    }
+}
+
+// Epilogue of a consumer wave: column c0 + wave*16 + col of sorted slots
+// row0 .. row0 + mrows - 1, gate tile 0 with up tile 1.
+template <int ACT, int MT>
+__device__ __forceinline__ void gateup_store(const GuArgs& A, const f32x4 (&acc)[2][MT], int c0, int row0, int mrows) {
+    const int wave = wave_id();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 15, c = lane >> 4;
     if (ACT == KSL_ACT_NONE) {
         // gate and up themselves, fp16, in plain column order: out1 [rows, 2I]
         const int64_t ld = 2 * static_cast<int64_t>(A.I);
-        f16* o = A.out2 + (static_cast<int64_t>(start + m0) + 4 * c) * ld + c0 + wave * 16 + col;
+        f16* o = A.out2 + (static_cast<int64_t>(row0) + 4 * c) * ld + c0 + wave * 16 + col;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -347,7 +353,7 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
         const int sc = out2_store_index(c0 + wave * 16 + col, A.I & ~127);  // out2 is the down GEMM's activation
         // the lane's part of the row offset (4c rows) in its pointer, the
         // uniform part ((16t + q) rows) as a scalar offset
-        f16* o = A.out2 + (static_cast<int64_t>(start + m0) + 4 * c) * A.I + sc;
+        f16* o = A.out2 + (static_cast<int64_t>(row0) + 4 * c) * A.I + sc;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -357,6 +363,28 @@ __device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const ch
                     o[(t * 16 + q) * A.I] = static_cast<f16>(act_times_up<ACT>(acc[0][t][q], acc[1][t][q]));
             }
     }
+}
+
+// Consumer side of one row chunk: 1 + G barriers, matching gateup_produce.
+template <int ACT, int NC, int NP, int R, int MT>
+__device__ __forceinline__ void gateup_consume(const GuArgs& A, int c0, const char* __restrict__ lds,
+                                               const f16* __restrict__ lds_sz, int start, int m0, int mrows) {
+    using S = GuShape<NC, NP, R>;
+    const int G = A.H >> 7;
+    const NibConsts kn = nib_consts();
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();  // group 0 and the scale table are ready
+    int slot = 0;
+    for (int g = 0; g < G; ++g) {
+        gateup_group<NC, MT>(lds + slot * S::kSlot, lds_sz, G, g, kn, acc);
+        slot = slot + 1 == R ? 0 : slot + 1;
+        __syncthreads();
+    }
+    gateup_store<ACT, MT>(A, acc, c0, start + m0, mrows);
 }
 
 template <int ACT, int NC, int NP, int R>
@@ -431,6 +459,421 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
     }
 }
 
+// ------------------------------------------------ gate/up, flowing ring
+// Persistent form of the 11 + 1-wave kernel above (NC consumers, one producer,
+// ring depth 3) for launches with more (expert, column block) items than CUs:
+// W workgroups (one per CU), workgroup w owns the items w, w + W, w + 2W, ...
+// of gateup_act_kernel's numbering (all column blocks of an expert on one XCD
+// while W is a multiple of 8). Every item is cut into passes of up to 32 rows,
+// and the producer streams the quantisation groups of all the workgroup's
+// passes through one ring without draining it between them: the ring fills
+// once per workgroup instead of once per item, and the first groups of the
+// next pass land while the consumers finish the current one. While they
+// compute, the consumers also fetch what the next pass needs into spare LDS:
+// the token ids of its rows, and the scale / zero table when it starts a new
+// item (two table buffers, alternating per item with rows).
+// Balanced pairs: with exactly two items per workgroup and whole experts in
+// each XCD's first-round items, the second item is not w + W: the first-round
+// experts ranked by rows (most first) are matched with the second-round
+// experts ranked the other way (fewest first), so a workgroup with a heavy
+// first item gets a light second one. The column blocks of a matched expert
+// follow those of its partner, so they stay together on one XCD.
+// Arithmetic and outputs are those of gateup_act_kernel, bit for bit.
+constexpr int kFlowMaxItems = 64;  // items per workgroup (table entries)
+// int32 read through the constant address space: uniform loads become scalar
+// loads (counted by lgkmcnt, not by the vmcnt of the direct-to-LDS loads)
+using ConstI32 = const int32_t __attribute__((address_space(4)));
+__device__ __forceinline__ const ConstI32* as_scalar_i32(const int32_t* p) { return (const ConstI32*)p; }
+constexpr int kFlowR = 3;          // ring depth
+constexpr int kFlowMinG = 8;       // groups per pass: the next pass's token ids go
+                                   // to LDS at group G/2, its first issue is at G-2
+
+template <int NC>
+struct GuFlowShape {
+    using B = GuShape<NC, 1, kFlowR>;
+    static constexpr size_t sz_bytes(int G) { return static_cast<size_t>(4) * B::kCols * G * 2; }
+    static constexpr size_t sz_off(int G, int buf) { return static_cast<size_t>(kFlowR) * B::kSlot + buf * sz_bytes(G); }
+    static constexpr size_t tok_off(int G) { return sz_off(G, 2); }
+    // item table: (first sorted slot, rows, expert, first column) per item
+    static constexpr size_t info_off(int G) { return tok_off(G) + 2 * 16 * kMaxMt * 4; }
+    static constexpr size_t lds_bytes(int G) { return info_off(G) + kFlowMaxItems * 16; }
+};
+
+// Item table of workgroup w, written by the calling wave (wave 0 of the
+// consumers): (first sorted slot, rows, expert, first column) of items
+// 0 .. K-1. Without pairs item k is w + k*W. With balanced pairs (K = 2,
+// W = items / 2, n = W / nb <= 64 experts per round, one per lane): lane j
+// holds the expert of the first-round workgroup 8*nb*(j/8) + j%8 (column
+// block 0) and the expert of that workgroup's natural second item; the
+// caller's first item is the expert of lane jm, column block b, and its rank r
+// among the first-round experts (most rows first, ties: lower expert first)
+// picks the second-round expert of rank r (fewest rows first, same ties),
+// column block b. All loads go out before any is used.
+__device__ __forceinline__ void gu_flow_fill_table(const GuArgs& A, int4* __restrict__ info, int w, int W, int items,
+                                                   int K, int nb, int kCols, bool pair) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (!pair) {
+        if (lane < K) {
+            const int tile = xcd_remap(w + lane * W, items);
+            const int e = tile / nb;
+            const int start = A.offsets[e];
+            info[lane] = int4{start, A.offsets[e + 1] - start, e, (tile - e * nb) * kCols};
+        }
+        return;
+    }
+    const int n = W / nb;
+    const int wj = 8 * nb * (lane >> 3) + (lane & 7);
+    int e1 = 0, e2 = 0, s1 = 0, s2 = 0, m1 = -1, m2 = 0x7fffffff;
+    if (lane < n) {
+        e1 = xcd_remap(wj, items) / nb;
+        e2 = xcd_remap(wj + W, items) / nb;
+        s1 = A.offsets[e1];
+        s2 = A.offsets[e2];
+        m1 = A.offsets[e1 + 1] - s1;
+        m2 = A.offsets[e2 + 1] - s2;
+    }
+    const int q = w >> 3;
+    const int b = q % nb;
+    const int jm = (q / nb) * 8 + (w & 7);
+    const int m1me = __builtin_amdgcn_readlane(m1, jm), e1me = __builtin_amdgcn_readlane(e1, jm);
+    const int r = __popcll(__ballot(lane < n && (m1 > m1me || (m1 == m1me && e1 < e1me))));
+    int rank2 = 0;
+    for (int k = 0; k < n; ++k) {
+        const int mk = __builtin_amdgcn_readlane(m2, k), ek = __builtin_amdgcn_readlane(e2, k);
+        rank2 += (mk < m2 || (mk == m2 && ek < e2)) ? 1 : 0;
+    }
+    const int jl = __ffsll(static_cast<unsigned long long>(__ballot(lane < n && rank2 == r))) - 1;  // one lane
+    const int4 first{__builtin_amdgcn_readlane(s1, jm), m1me, e1me, b * kCols};
+    const int4 second{__builtin_amdgcn_readlane(s2, jl), __builtin_amdgcn_readlane(m2, jl),
+                      __builtin_amdgcn_readlane(e2, jl), b * kCols};
+    if (lane == 0) info[0] = first;
+    if (lane == 1) info[1] = second;
+}
+
+// A pass: rows start + m0 .. start + min(M, m0 + 32) - 1 of item k (k == K: none left).
+struct GuPass {
+    int k, m0, start, M;
+};
+
+// The item table held in registers after the first barrier: lane k holds
+// item k (one LDS read per wave); entries are then taken with v_readlane,
+// without LDS round trips at the pass changes.
+__device__ __forceinline__ int4 gu_flow_table(const int4* info, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    return lane < K ? info[lane] : int4{0, 0, 0, 0};
+}
+
+// The first pass at or after (k, m0) with rows. All values wave-uniform.
+__device__ __forceinline__ GuPass gu_flow_seek(int k, int m0, int K, const int4& tab) {
+    while (k < K) {
+        const int start = __builtin_amdgcn_readlane(tab.x, k), M = __builtin_amdgcn_readlane(tab.y, k);
+        if (m0 < M) return GuPass{k, m0, start, M};
+        ++k;
+        m0 = 0;
+    }
+    return GuPass{K, 0, 0, 0};
+}
+
+__device__ __forceinline__ int gu_flow_npass(int K, const int4& tab) {
+    int n = 0;
+    for (int k = 0; k < K; ++k) n += (__builtin_amdgcn_readlane(tab.y, k) + 16 * kMaxMt - 1) / (16 * kMaxMt);
+    return n;
+}
+
+__device__ __forceinline__ void gu_flow_item(const int4& tab, int k, int& e, int& c0) {
+    e = __builtin_amdgcn_readlane(tab.z, k);
+    c0 = __builtin_amdgcn_readlane(tab.w, k);
+}
+
+// The scale / zero table of an item's kCols rows: four [kCols x G] fp16 blocks
+// (s_gate, z_gate, s_up, z_up), each contiguous in global memory, fetched by
+// the consumer threads into registers (issue) and written to LDS (commit).
+template <int NC>
+struct GuSzFetch {
+    using S = GuShape<NC, 1, kFlowR>;
+    u32x4 v[S::kSzPer];
+    // chunk k of this thread: 16 bytes of block b at o, or none
+    __device__ __forceinline__ static const u32x4* src(const GuArgs& A, int e, int c0, int G, int k) {
+        const int nq = S::kCols * G * 2 / 16;  // 16-byte chunks per block
+        int i = threadIdx.x + k * NC * kWave;
+        if (i >= 4 * nq) i = 0;  // clamped, never stored
+        const int64_t gate0 = static_cast<int64_t>(e) * 2 * A.I + c0;
+        const int b = i / nq, o = i - b * nq;
+        const f16* base = ((b & 1) ? A.gu_z : A.gu_s) + ((b & 2) ? gate0 + A.I : gate0) * G;
+        return reinterpret_cast<const u32x4*>(base) + o;
+    }
+    __device__ __forceinline__ void issue(const GuArgs& A, int e, int c0, int G) {
+#pragma unroll
+        for (int k = 0; k < S::kSzPer; ++k) v[k] = *src(A, e, c0, G, k);
+    }
+    __device__ __forceinline__ void commit(f16* __restrict__ dst, int G) const {
+        const int nq = S::kCols * G * 2 / 16;
+#pragma unroll
+        for (int k = 0; k < S::kSzPer; ++k) {
+            const int i = threadIdx.x + k * NC * kWave;
+            if (i < 4 * nq) reinterpret_cast<u32x4*>(dst)[i] = v[k];
+        }
+    }
+};
+
+template <int NC>
+__device__ __forceinline__ void gu_flow_produce(const GuArgs& A, char* __restrict__ lds, int w, int items, int K) {
+    using S = GuShape<NC, 1, kFlowR>;
+    using F = GuFlowShape<NC>;
+    constexpr int R = kFlowR;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int rr = lane >> 2, ch = (lane & 3) ^ frag_swz(rr);
+    const int G = A.H >> 7;
+    const int nb = A.I / S::kCols;
+    const int rowbytes = A.H >> 1;
+    const int wlane = rr * rowbytes + ch * 16;
+    const int* tok = reinterpret_cast<const int*>(lds + F::tok_off(G));
+    const int4* info = reinterpret_cast<const int4*>(lds + F::info_off(G));
+    const char* abase = reinterpret_cast<const char*>(A.a16);
+    // the issue cursor's pass: weights of its item (first gate row + the lane's
+    // piece), the lane's activation row of each M tile, its M tiles
+    const char* wbase = nullptr;
+    int64_t aoff[kMaxMt];
+    int mt = 1;
+    auto set_item = [&](int e, int c0) {
+        wbase = reinterpret_cast<const char*>(A.gu_q) + (static_cast<int64_t>(e) * 2 * A.I + c0) * rowbytes + wlane;
+    };
+    // token row of M tile t of pass p for this lane (rows past the pass's last
+    // repeat it: loaded, never stored): from the consumers' LDS copy (toks)
+    // for all passes but a workgroup's first
+    auto set_rows = [&](const GuPass& p, const int* toks) {
+        const int mrows = min(p.M - p.m0, 16 * kMaxMt);
+        mt = mrows > 16 ? 2 : 1;
+#pragma unroll
+        for (int t = 0; t < kMaxMt; ++t) aoff[t] = (static_cast<int64_t>(toks[t * 16 + rr]) * A.H + ch * 8) * 2;
+    };
+    // ... and for the first pass from the routing itself, by scalar loads: a
+    // vector load here would wait (in-order vmcnt) for the weight groups
+    // already in flight
+    auto set_rows_first = [&](const GuPass& p) {
+        const int mrows = min(p.M - p.m0, 16 * kMaxMt);
+        mt = mrows > 16 ? 2 : 1;
+        const ConstI32* rows = as_scalar_i32(A.sorted_rows) + p.start + p.m0;
+        int v[16 * kMaxMt];  // all loads first (uniform, in flight together), then a per-lane pick
+#pragma unroll
+        for (int i = 0; i < 16 * kMaxMt; ++i) v[i] = rows[min(i, mrows - 1)];
+#pragma unroll
+        for (int i = 0; i < 16 * kMaxMt; ++i) asm volatile("" : "+s"(v[i]));  // not folded into a per-lane load
+#pragma unroll
+        for (int t = 0; t < kMaxMt; ++t) {
+            int row = v[t * 16];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) row = rr == i ? v[t * 16 + i] : row;
+            aoff[t] = (static_cast<int64_t>(row / A.topk) * A.H + ch * 8) * 2;
+        }
+    };
+    auto issue_w = [&](int g, int slot) {
+        char* base = lds + slot * S::kSlot;
+#pragma unroll
+        for (int b = 0; b < 2 * NC; ++b) {
+            const int wv = b >> 1, j = b & 1;
+            dma16(wbase + static_cast<int64_t>((j ? A.I : 0) + wv * 16) * rowbytes + g * 64, base + b * kBlk);
+        }
+    };
+    auto issue_a = [&](int g, int slot) {
+        char* base = lds + slot * S::kSlot;
+#pragma unroll
+        for (int t = 0; t < kMaxMt; ++t)
+            if (t < mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    dma16(abase + aoff[t] + (i * 32 + g * 128) * 2, base + (2 * NC + t * 4 + i) * kBlk);
+    };
+
+    // prologue. The first item is known without the table (item w): its first
+    // weight groups go out before the routing is read. When it has no rows,
+    // the first pass is found in the table after the first barrier and one
+    // more barrier publishes its first group (the consumers take it too).
+    const int t0 = xcd_remap(w, items);
+    const int e0 = t0 / nb;
+    set_item(e0, (t0 - e0 * nb) * S::kCols);
+    const bool early = A.early != 0;
+    if (early)
+        for (int g = 0; g < R - 1; ++g) issue_w(g, g);
+    const ConstI32* offs = as_scalar_i32(A.offsets);  // scalar loads, as above
+    const int start0 = offs[e0];
+    GuPass p{0, 0, start0, offs[e0 + 1] - start0};
+    const bool first_rows = p.M > 0;
+    if (first_rows) {
+        set_rows_first(p);
+        for (int g = 0; g < R - 1; ++g) {
+            if (!early) issue_w(g, g);
+            issue_a(g, g);
+        }
+    }
+    vm_wait<0>();
+    dma_barrier();
+    const int4 tab = gu_flow_table(info, K);
+    const int S_total = gu_flow_npass(K, tab) * G;  // group steps of all passes
+    if (!first_rows && S_total > 0) {
+        p = gu_flow_seek(0, 0, K, tab);
+        int e, c0;
+        gu_flow_item(tab, p.k, e, c0);
+        set_item(e, c0);
+        set_rows_first(p);
+        for (int g = 0; g < R - 1; ++g) {
+            issue_w(g, g);
+            issue_a(g, g);
+        }
+        vm_wait<0>();
+        dma_barrier();
+    }
+    int ig = R - 1;      // group of the issue cursor's pass
+    int ipass = 0;       // ordinal of the issue cursor's pass
+    int slot_i = R - 1;  // slot of the next issue
+    int issued = S_total > 0 ? R - 1 : 0;
+    for (int s = 0; s < S_total; ++s) {
+        // consumers read step s from slot s % R; the slot of step s - 1 is free
+        int mt_issued = 0;
+        if (issued < S_total) {
+            if (ig == G) {  // the issue cursor enters the next pass
+                const GuPass q = gu_flow_seek(p.k, p.m0 + 16 * kMaxMt, K, tab);
+                if (q.k != p.k) {
+                    int e, c0;
+                    gu_flow_item(tab, q.k, e, c0);
+                    set_item(e, c0);
+                }
+                p = q;
+                ++ipass;
+                ig = 0;
+                set_rows(p, tok + (ipass & 1) * 16 * kMaxMt);
+            }
+            issue_w(ig, slot_i);
+            issue_a(ig, slot_i);
+            mt_issued = mt;
+            ++ig;
+            ++issued;
+            slot_i = slot_i + 1 == R ? 0 : slot_i + 1;
+        }
+        // step s + 1 must have landed before the barrier: only the step just
+        // issued (2*NC + 4*mt loads) may still be in flight
+        if (mt_issued == 1)
+            vm_wait<2 * NC + 4>();
+        else if (mt_issued == 2)
+            vm_wait<2 * NC + 8>();
+        else
+            vm_wait<0>();
+        dma_barrier();
+    }
+    vm_wait<0>();
+}
+
+// Consumer side of one pass: G barriers. At group 1 the loads for the next pass
+// go out (the expanded rows of its slots from wave 0; the scale / zero table
+// of its item when it starts a new one), at group G/2 they go to LDS.
+template <int ACT, int NC, int MT>
+__device__ __forceinline__ void gu_flow_consume_pass(const GuArgs& A, char* __restrict__ lds, int& slot,
+                                                     const f16* __restrict__ sz, int c0, int row0, int mrows,
+                                                     int nrow0, int nmrows, int* __restrict__ ntok, int ne, int nc0,
+                                                     f16* __restrict__ nsz) {
+    using S = GuShape<NC, 1, kFlowR>;
+    const int G = A.H >> 7;
+    const int tid = threadIdx.x;
+    const NibConsts kn = nib_consts();
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    GuSzFetch<NC> nf;
+    int row = 0;
+    for (int g = 0; g < G; ++g) {
+        gateup_group<NC, MT>(lds + slot * S::kSlot, sz, G, g, kn, acc);
+        if (g == 1) {
+            // the expanded row only: its token (row / topk) is taken at G/2, once it has landed
+            if (ntok && tid < 16 * kMaxMt) row = A.sorted_rows[nrow0 + min(tid, nmrows - 1)];
+            if (nsz) nf.issue(A, ne, nc0, G);
+        } else if (g == G / 2) {
+            if (ntok && tid < 16 * kMaxMt) ntok[tid] = row / A.topk;
+            if (nsz) nf.commit(nsz, G);
+        }
+        slot = slot + 1 == kFlowR ? 0 : slot + 1;
+        __syncthreads();
+    }
+    // the prefetch registers landed at G/2; an explicit wait tells the
+    // compiler so (it cannot pair the two conditional blocks), else it waits
+    // for this epilogue's stores before reusing those registers in the next pass
+    vm_wait<0>();
+    gateup_store<ACT, MT>(A, acc, c0, row0, mrows);
+}
+
+template <int ACT, int NC>
+__device__ __forceinline__ void gu_flow_consume(const GuArgs& A, char* __restrict__ lds, int w, int W, int items,
+                                                int K, bool pair) {
+    using S = GuShape<NC, 1, kFlowR>;
+    using F = GuFlowShape<NC>;
+    const int G = A.H >> 7;
+    const int nb = A.I / S::kCols;
+    int* tok = reinterpret_cast<int*>(lds + F::tok_off(G));
+    int4* info = reinterpret_cast<int4*>(lds + F::info_off(G));
+    f16* sz0 = reinterpret_cast<f16*>(lds + F::sz_off(G, 0));
+    // the first item's scale / zero table into buffer 0, issued first (item w,
+    // known without the table; read in vain when it has no rows), then the
+    // item table by wave 0, whose routing loads overlap the table's
+    const int t0 = xcd_remap(w, items);
+    const int e0 = t0 / nb;
+    {
+        GuSzFetch<NC> f;
+        f.issue(A, e0, (t0 - e0 * nb) * S::kCols, G);
+        if (wave_id() == 0) gu_flow_fill_table(A, info, w, W, items, K, nb, S::kCols, pair);
+        f.commit(sz0, G);
+    }
+    __syncthreads();  // first barrier: the table, buffer 0 and the first pass's group 0 are ready
+    const int4 tab = gu_flow_table(info, K);
+    const int npass = gu_flow_npass(K, tab);
+    GuPass p = gu_flow_seek(0, 0, K, tab);
+    const bool first_rows = __builtin_amdgcn_readlane(tab.y, 0) > 0;
+    if (!first_rows && npass > 0) {  // the first pass is a later item's (one more barrier, as the producer)
+        int e, c0;
+        gu_flow_item(tab, p.k, e, c0);
+        GuSzFetch<NC> f;
+        f.issue(A, e, c0, G);
+        f.commit(sz0, G);
+        __syncthreads();
+    }
+    int zb = 0;  // table buffer of the current item
+    int slot = 0;
+    for (int ip = 0; ip < npass; ++ip) {
+        const GuPass q = gu_flow_seek(p.k, p.m0 + 16 * kMaxMt, K, tab);
+        const bool more = q.k < K, fresh = more && q.k != p.k;
+        int e, c0, ne = 0, nc0 = 0;
+        gu_flow_item(tab, p.k, e, c0);
+        if (fresh) gu_flow_item(tab, q.k, ne, nc0);
+        const f16* sz = reinterpret_cast<const f16*>(lds + F::sz_off(G, zb));
+        int* ntok = more ? tok + ((ip + 1) & 1) * 16 * kMaxMt : nullptr;
+        f16* nsz = fresh ? reinterpret_cast<f16*>(lds + F::sz_off(G, zb ^ 1)) : nullptr;
+        const int mrows = min(p.M - p.m0, 16 * kMaxMt);
+        const int nrow0 = q.start + q.m0, nmrows = more ? min(q.M - q.m0, 16 * kMaxMt) : 1;
+        if (mrows <= 16)
+            gu_flow_consume_pass<ACT, NC, 1>(A, lds, slot, sz, c0, p.start + p.m0, mrows, nrow0, nmrows, ntok, ne, nc0,
+                                             nsz);
+        else
+            gu_flow_consume_pass<ACT, NC, 2>(A, lds, slot, sz, c0, p.start + p.m0, mrows, nrow0, nmrows, ntok, ne, nc0,
+                                             nsz);
+        if (fresh) zb ^= 1;
+        p = q;
+    }
+}
+
+template <int ACT, int NC>
+__global__ __launch_bounds__((NC + 1) * kWave) void gateup_flow_kernel(GuArgs A, int W, int items, int pair) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int w = blockIdx.x;
+    const int K = (items - w + W - 1) / W;  // items of this workgroup (1 .. kFlowMaxItems)
+    if (wave_id() >= NC) {
+        // the producer issues first on its SIMD after each barrier
+        __builtin_amdgcn_s_setprio(3);
+        gu_flow_produce<NC>(A, lds, w, items, K);
+    } else {
+        gu_flow_consume<ACT, NC>(A, lds, w, W, items, K, pair != 0);
+    }
+}
+
 // Dynamic LDS beyond 64 KB: raise a kernel's limit (called once per kernel).
 bool set_max_lds(const void* fn) {
     const bool ok = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsDynMax) == hipSuccess;
@@ -481,6 +924,48 @@ int launch_gateup_nc(const GuArgs& A, int64_t E, int64_t nrows, int act, hipStre
         return KSL_ERR_ARG;
     KSL_LAUNCH_CHECK();
     return KSL_OK;
+}
+
+template <int NC>
+int launch_gateup_flow(const GuArgs& A, int act, int W, int items, hipStream_t st) {
+    using F = GuFlowShape<NC>;
+    constexpr int kThreads = (NC + 1) * kWave;
+    const size_t lds = F::lds_bytes(A.H / 128);
+    if (lds > kLdsDynMax) return KSL_ERR_SHAPE;
+    // balanced pairs: two items per workgroup, whole experts in each XCD's
+    // first-round items, at most one first-round expert per lane of a wave
+    const int nb = A.I / GuShape<NC, 1, kFlowR>::kCols;
+    const int pair = items == 2 * W && (W / kXcds) % nb == 0 && (items / kXcds) % nb == 0 && W / nb <= kWave;
+    static const bool attr_set =
+        set_max_lds(reinterpret_cast<const void*>(&gateup_flow_kernel<KSL_ACT_GELU_TANH, NC>)) &&
+        set_max_lds(reinterpret_cast<const void*>(&gateup_flow_kernel<KSL_ACT_SILU, NC>)) &&
+        set_max_lds(reinterpret_cast<const void*>(&gateup_flow_kernel<KSL_ACT_NONE, NC>));
+    (void)attr_set;
+    if (act == KSL_ACT_GELU_TANH)
+        hipLaunchKernelGGL((gateup_flow_kernel<KSL_ACT_GELU_TANH, NC>), dim3(W), dim3(kThreads), lds, st, A, W, items,
+                           pair);
+    else if (act == KSL_ACT_SILU)
+        hipLaunchKernelGGL((gateup_flow_kernel<KSL_ACT_SILU, NC>), dim3(W), dim3(kThreads), lds, st, A, W, items, pair);
+    else if (act == KSL_ACT_NONE)
+        hipLaunchKernelGGL((gateup_flow_kernel<KSL_ACT_NONE, NC>), dim3(W), dim3(kThreads), lds, st, A, W, items, pair);
+    else
+        return KSL_ERR_ARG;
+    KSL_LAUNCH_CHECK();
+    return KSL_OK;
+}
+
+// Workgroups of the flowing gate/up launch for `items` (expert, column block)
+// items, H/128 groups per pass: one per CU (a multiple of 8, so an expert's
+// column blocks share an XCD), or 0 where the launch of one workgroup per item
+// is used instead (no more items than CUs, short passes, more items per
+// workgroup than the item table holds, or LDS).
+int gateup_flow_workgroups(int64_t items, int64_t H, int cus) {
+    constexpr int NC = 11;
+    const int W = cus - cus % kXcds;
+    const int G = static_cast<int>(H / 128);
+    if (W < kXcds || items <= cus || items > static_cast<int64_t>(W) * kFlowMaxItems) return 0;
+    if (G < kFlowMinG || GuFlowShape<NC>::lds_bytes(G) > kLdsDynMax) return 0;
+    return W;
 }
 
 // --------------------------------------------------------------------- down
@@ -568,16 +1053,6 @@ struct DnTile {
         else return __builtin_bit_cast(f16, static_cast<uint16_t>(z[j]));
     }
 };
-
-// Compile-time loop: f(integral_constant<int, 0>) .. f(integral_constant<int, N-1>).
-template <int N, typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-    (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
-}
 
 // Per-lane byte offsets of a tile's loads, the same for every tile (kept in
 // registers across the walk, so that a fetch only changes wave-uniform bases).
@@ -986,6 +1461,11 @@ int launch_gateup(const void* a16, const int32_t* sorted_rows, const int32_t* of
     // producer wave (12 waves, 3 per SIMD), ring depth 3
     if (I % 176 == 0) {
         static_assert(GuShape<11, 1, 3>::lds_bytes(kGuMaxG) <= kLdsDynMax, "gate/up LDS");
+        // more items than CUs: one persistent workgroup per CU, the ring
+        // flowing across its items
+        const int64_t items = E * (I / 176);
+        const int W = gateup_flow_workgroups(items, H, device_cus());
+        if (W > 0) return launch_gateup_flow<11>(A, act, W, static_cast<int>(items), st);
         return launch_gateup_nc<11, 1, 3>(A, E, nrows_hint, act, st);
     }
     if (I % 128 == 0) return launch_gateup_nc<8, 4, 4>(A, E, nrows_hint, act, st);

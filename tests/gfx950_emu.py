@@ -18,8 +18,9 @@ It runs one wave with concrete kernel arguments and tracks:
 - every global, buffer and LDS access, checked against the buffers and LDS
   size of the launch, and whether any address, stored value or MFMA operand
   is poisoned.
-Barriers are no-ops: the waves of a workgroup run one after another, sharing
-LDS (the code checked here publishes only routing scalars through LDS)."""
+Barriers are counted, not waited on: the waves of a workgroup run one after
+another, sharing LDS (the code checked here publishes only routing scalars and
+row tables through LDS), and a test compares the waves' barrier counts."""
 import re, struct, sys
 import numpy as np
 
@@ -61,6 +62,7 @@ class Wave:
         self.vmq = []  # outstanding vmem ops: [dest vgpr set, set of dests written since issue]
         self.poison = np.zeros(256, dtype=bool)  # register may hold a stale or clobbered value
         self.spoison = [False] * 128
+        self.barriers = 0  # s_barrier instructions executed (all waves of a workgroup must agree)
     # ---- operand helpers
     def sreg(self, t):
         m = re.match(r"s\[(\d+):(\d+)\]$", t)
@@ -198,7 +200,9 @@ def run(ins, labels, w, max_steps=2_000_000):
                         w.poison[r] = r in written  # a landing after a newer write clobbers it
                         if r in written and len(w.trace) < 8: w.trace.append(("CLOBBER at wait", w.cur, r))
             continue
-        if op in ("s_nop", "s_barrier", "s_setprio", "s_sleep") : continue
+        if op == "s_barrier":
+            w.barriers += 1; continue
+        if op in ("s_nop", "s_setprio", "s_sleep") : continue
         if op == "s_branch": pc = labels[t[0]]; continue
         if op.startswith("s_cbranch"):
             cond = op[len("s_cbranch_"):]
@@ -222,8 +226,11 @@ def run(ins, labels, w, max_steps=2_000_000):
             continue
         if op.startswith("s_load"):
             n = {"s_load_dword": 1, "s_load_dwordx2": 2, "s_load_dwordx4": 4, "s_load_dwordx8": 8}[op]
-            base = w.sget(t[1], 2); off = int(t[2], 0)
-            addr = base + off
+            base = w.sget(t[1], 2)
+            off = w.sget(t[2]) if t[2].startswith("s") else int(t[2], 0)  # soffset register or immediate
+            for x in t[3:]:
+                if x.startswith("offset:"): off += int(x[7:], 0)
+            addr = (base + off) & 0xFFFFFFFFFFFFFFFF
             ok = any(lo <= addr and addr + 4 * n <= hi for (lo, hi) in w.buffers.values()) or addr in w.mem
             vals = [w.mem.get(addr + 4 * k) for k in range(n)]
             for k, r in enumerate(w.sreg(t[0])):
@@ -313,6 +320,18 @@ def run(ins, labels, w, max_steps=2_000_000):
                     if i in q[0]: q[1].add(i)
                 w.poison[i] = pz
             w.vmq.append([set(r), set()]); continue
+        if op.startswith("global_store"):
+            size = {"global_store_byte": 1, "global_store_short": 2, "global_store_dword": 4,
+                    "global_store_dwordx2": 8, "global_store_dwordx4": 16}[op]
+            if w.check_inflight_read(t[1]): w.errors.append(("STALE DATA stored", w.cur))
+            if w.check_inflight_read(t[0]): w.errors.append(("POISONED ADDRESS store", w.cur))
+            addr, kn = gaddr(w, t[0], t[2])
+            off = 0
+            for x in t[3:]:
+                if x.startswith("offset:"): off = int(x[7:], 0)
+            addr = np.array([(int(a) + off) & 0xFFFFFFFFFFFFFFFF for a in addr], dtype=U64)
+            w.check_addr(addr, kn, size, op, w.act())
+            w.vmq.append([set(), set()]); continue
         if op.startswith("buffer_store"):
             n = {"buffer_store_dword": 1, "buffer_store_dwordx2": 2, "buffer_store_dwordx4": 4}[op]
             if w.check_inflight_read(t[0]): w.errors.append(("STALE DATA stored", w.cur))
@@ -458,8 +477,8 @@ def run(ins, labels, w, max_steps=2_000_000):
         if op.startswith("v_"):
             w.cur_poison = any(w.check_inflight_read(x) for x in t[1:])
             vop(w, op, t)
-            if op.startswith("v_readfirstlane"):
-                for i in w.sreg(t[0]): w.spoison[i] = w.cur_poison
+            if op.startswith("v_readfirstlane") or op.startswith("v_readlane"):
+                for i in (w.sreg(t[0]) or []): w.spoison[i] = w.cur_poison  # (vcc_lo, m0: not tracked)
             if op.startswith("v_cmp") and not op.endswith("_e32") and w.sreg(t[0]):
                 w.cur_poison = any(w.check_inflight_read(x) for x in t[1:])
                 for i in w.sreg(t[0]): w.spoison[i] = w.cur_poison
@@ -500,14 +519,18 @@ def sop(w, op, t):
     if op == "s_and_b64": r = g(t[1], 2) & g(t[2], 2); w.sset(t[0], r, 2); w.scc = int(r != 0); return
     if op == "s_or_b64": r = g(t[1], 2) | g(t[2], 2); w.sset(t[0], r, 2); w.scc = int(r != 0); return
     if op == "s_xor_b64": r = (g(t[1], 2) ^ g(t[2], 2)) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
+    if op == "s_nor_b64": r = ~(g(t[1], 2) | g(t[2], 2)) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
+    if op == "s_nand_b64": r = ~(g(t[1], 2) & g(t[2], 2)) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
+    if op == "s_xnor_b64": r = ~(g(t[1], 2) ^ g(t[2], 2)) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
+    if op == "s_not_b64": r = ~g(t[1], 2) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
     if op == "s_andn2_b64": r = g(t[1], 2) & ~g(t[2], 2) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
     if op == "s_orn2_b64": r = (g(t[1], 2) | ~g(t[2], 2)) & 0xFFFFFFFFFFFFFFFF; w.sset(t[0], r, 2); w.scc = int(r != 0); return
     if op == "s_and_saveexec_b64":
-        old = w.exec; w.sset(t[0], old, 2); w.exec = old & g(t[1], 2); w.scc = int(w.exec != 0); return
+        src, old = g(t[1], 2), w.exec; w.sset(t[0], old, 2); w.exec = old & src; w.scc = int(w.exec != 0); return
     if op == "s_andn2_saveexec_b64":
-        old = w.exec; w.sset(t[0], old, 2); w.exec = g(t[1], 2) & ~old & 0xFFFFFFFFFFFFFFFF; w.scc = int(w.exec != 0); return
+        src, old = g(t[1], 2), w.exec; w.sset(t[0], old, 2); w.exec = src & ~old & 0xFFFFFFFFFFFFFFFF; w.scc = int(w.exec != 0); return
     if op == "s_or_saveexec_b64":
-        old = w.exec; w.sset(t[0], old, 2); w.exec = g(t[1], 2) | old; w.scc = int(w.exec != 0); return
+        src, old = g(t[1], 2), w.exec; w.sset(t[0], old, 2); w.exec = src | old; w.scc = int(w.exec != 0); return
     if op == "s_brev_b32": w.sset(t[0], int(f"{g(t[1]) & M32:032b}"[::-1], 2)); return
     if op == "s_abs_i32": r = abs(signed32(g(t[1]))) & M32; w.sset(t[0], r); w.scc = int(r != 0); return
     if op in ("s_min_i32", "s_max_i32"):
@@ -515,6 +538,11 @@ def sop(w, op, t):
         w.sset(t[0], r & M32); w.scc = int(r == a); return
     if op in ("s_min_u32", "s_max_u32"):
         a, b = g(t[1]), g(t[2]); r = min(a, b) if op == "s_min_u32" else max(a, b); w.sset(t[0], r); return
+    if op.startswith("s_cmpk_"):  # 16-bit immediate: sign-extended for _i32, zero-extended for _u32
+        kind = op[7:]
+        a, b = g(t[0]), int(t[1], 0) & 0xFFFF
+        if kind.endswith("i32"): a, b = signed32(a), (b - 0x10000 if b & 0x8000 else b)
+        w.scc = int({"eq": a == b, "lg": a != b, "lt": a < b, "le": a <= b, "gt": a > b, "ge": a >= b}[kind[:2]]); return
     if op.startswith("s_cmp_"):
         kind = op[6:]
         a, b = g(t[0]), g(t[1])
@@ -528,6 +556,11 @@ def sop(w, op, t):
         w.sset(t[0], a if w.scc else b, 2); return
     if op == "s_bfe_u32":
         v = g(t[2]); off, wd = v & 31, (v >> 16) & 127; w.sset(t[0], (g(t[1]) >> off) & ((1 << wd) - 1)); return
+    if op in ("s_bcnt1_i32_b64", "s_bcnt1_i32_b32"):
+        r = bin(g(t[1], 2 if op.endswith("b64") else 1)).count("1"); w.sset(t[0], r); w.scc = int(r != 0); return
+    if op in ("s_ff1_i32_b64", "s_ff1_i32_b32"):
+        v = g(t[1], 2 if op.endswith("b64") else 1)
+        w.sset(t[0], (v & -v).bit_length() - 1 if v else M32); return
     if op == "s_getreg_b32": w.sset(t[0], 0); return
     if op == "s_getpc_b64": w.sset(t[0], 0, 2); return
     raise NotImplementedError(op + " " + " ".join(t))
@@ -652,7 +685,7 @@ def vop(w, op, t):
         else: a, ka = g(t[1]); b, kb = g(t[2]); m = w.sget(t[3], 2)
         sel = np.array([(m >> l) & 1 for l in range(NL)], dtype=bool)
         setv(np.where(sel, b, a) & MM, np.where(sel, kb, ka)); return
-    if base.startswith("v_cmp_"):
+    if base.startswith("v_cmp_") and not re.search(r"_(f32|f16|bf16)$", base):
         kind = base[6:]
         c, ty = kind.split("_")
         if op.endswith("_e32"):
@@ -665,6 +698,20 @@ def vop(w, op, t):
         r = {"eq": a2 == b2, "ne": a2 != b2, "lt": a2 < b2, "le": a2 <= b2, "gt": a2 > b2, "ge": a2 >= b2}[c]
         if not (ka & kb)[act].all(): raise Unknown("cmp on unknown")
         w.sset(dst, w.mask_from(r & act), 2); return
+    if base == "v_writelane_b32":  # one lane, whatever exec (SGPR spill slots)
+        r = w.vreg(t[0])[0]
+        lane = int(w.sget(t[2])) & (NL - 1)
+        try:
+            val, known = w.sget(t[1]), True
+        except Unknown:
+            val, known = 0, False
+        w.v[r][lane] = U(val & M32); w.vk[r][lane] = known
+        w.poison[r] = w.poison[r] or w.cur_poison
+        return
+    if base == "v_readlane_b32":
+        a, ka = g(t[1])
+        lane = int(w.sget(t[2])) & (NL - 1)
+        w.sset(t[0], int(a[lane]) & M32, known=bool(ka[lane])); return
     if base == "v_readfirstlane_b32":
         a, ka = g(t[1])
         lanes = [l for l in range(NL) if act[l]]
@@ -681,12 +728,17 @@ def vop(w, op, t):
     if base == "v_cvt_f32_u32":
         a, ka = g(t[1]); r = np.array([f2u(float(np.float32(int(x)))) for x in a], dtype=U); setv(r, ka); return
     if base == "v_rcp_iflag_f32":
-        a, ka = g(t[1]); r = np.array([f2u(float(np.float32(1.0) / np.frombuffer(struct.pack('<I', int(x)), np.float32)[0])) if int(x) else 0x7f800000 for x in a], dtype=U); setv(r, ka); return
+        a, ka = g(t[1])
+        with np.errstate(all="ignore"):  # lanes of unknown value may hold any bits
+            r = np.array([f2u(float(np.float32(1.0) / np.frombuffer(struct.pack('<I', int(x)), np.float32)[0])) if int(x) else 0x7f800000 for x in a], dtype=U)
+        setv(r, ka); return
     if base == "v_mul_f32":
         a, ka = g(t[1]); b, kb = g(t[2])
         fa = np.array([np.frombuffer(struct.pack('<I', int(x) & M32), np.float32)[0] for x in a], dtype=np.float32)
         fb = np.array([np.frombuffer(struct.pack('<I', int(x) & M32), np.float32)[0] for x in b], dtype=np.float32)
-        r = np.array([f2u(float(x)) for x in (fa * fb)], dtype=U); setv(r, ka & kb); return
+        with np.errstate(all="ignore"):
+            r = np.array([f2u(float(x)) for x in (fa * fb)], dtype=U)
+        setv(r, ka & kb); return
     if base == "v_cvt_u32_f32":
         a, ka = g(t[1])
         fa = [np.frombuffer(struct.pack('<I', int(x) & M32), np.float32)[0] for x in a]
@@ -695,7 +747,21 @@ def vop(w, op, t):
     if base in ("v_add_f16", "v_cvt_pk_f16_f32", "v_add_f32", "v_fma_f32", "v_cvt_f16_f32", "v_mul_f16", "v_sub_f16",
                 "v_pk_add_f16", "v_pk_mul_f16", "v_pk_fma_f16", "v_accvgpr_read_b32", "v_accvgpr_write_b32", "v_exp_f32",
                 "v_max_f32", "v_min_f32", "v_cvt_f32_f16", "v_perm_b32", "v_pack_b32_f16", "v_fmac_f32", "v_sub_f32",
-                "v_cvt_pk_bf16_f32", "v_div_scale_f32", "v_rcp_f32"):
+                "v_cvt_pk_bf16_f32", "v_div_scale_f32", "v_rcp_f32", "v_fma_mix_f32", "v_fma_mixlo_f16",
+                "v_fma_mixhi_f16", "v_pk_mul_f32", "v_pk_add_f32", "v_pk_fma_f32"):
+        r = w.vreg(t[0])
+        for i in r:
+            w.vk[i] = np.where(act, False, w.vk[i])
+            for q in w.vmq:
+                if i in q[0]: q[1].add(i)
+            w.poison[i] = w.cur_poison
+        return
+    # other floating-point data ops (the activation epilogues): result unknown;
+    # a float compare only selects data (v_cndmask), never a branch or address
+    if re.search(r"_(f32|f16|bf16)$", base) or re.search(r"_(f32|f16)_", base):
+        if base.startswith("v_cmp"):
+            dst = "vcc" if t[0] == "vcc" or op.endswith("_e32") else t[0]
+            w.sset(dst, 0, 2); return
         r = w.vreg(t[0])
         for i in r:
             w.vk[i] = np.where(act, False, w.vk[i])

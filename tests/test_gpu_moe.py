@@ -318,6 +318,10 @@ STAGE_CASES = [
     (192, 2, 3, 256, 1024, 39),   # the largest I (16 64-groups)
     (1100, 8, 12, 256, 768, 40),  # 8800 rows: row blocks with I >= 768
     (8, 8, 128, 2816, 704, 41),   # 64 rows over 128 experts: most experts empty, one producer without early issue
+    # more (expert, column block) items than CUs: the persistent gate/up workgroups
+    (256, 8, 192, 2816, 704, 47),  # 768 items over 256 workgroups: three each, in order (no pairs)
+    (1024, 8, 128, 2816, 704, 48),  # 8192 rows: ~64 per expert, items of two and three passes, balanced pairs
+    (64, 4, 128, 1024, 704, 49),   # the shortest passes (8 groups), balanced pairs of mostly 1-16-row items
     # above 8192 rows, the GEMM-form row-block kernels (128-row blocks, full and partial)
     (1040, 8, 64, 2816, 704, 42),  # the layer's H and I: 6 down column blocks (the last half full), 64-K tail
     (1100, 8, 8, 384, 128, 43),    # three 128-groups of gate/up, one down group, 4 of 8 gate/up waves active
