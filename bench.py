@@ -25,7 +25,11 @@ Timed passes (all inside this process, on one stream):
      two HIP events on the same stream (the routing produced once; gate/up
      and down rotate over the weight sets), giving its average launch
      duration; achieved GB/s = the kernel's algorithmic bytes / that
-     duration, and the dominant kernel's is the roofline.
+     duration, and the dominant kernel's is the roofline. (Inside the layer,
+     after route_norm, rocprofv3 reads the persistent gate/up kernel's
+     dispatches ~4 us shorter than back to back; timing each stage inside the
+     layer with events between the launches adds ~2-3 us of launch gap per
+     stage instead, so the back-to-back figure stands.)
   3. RMSNorm alone at the rmsnorm_256 and rmsnorm_32k (+ qk-norm) shapes.
   4. cpu_baseline: the reference CPU path (torch eager, oracle/cpu_baseline.py)
      on every host core of the process's affinity set, bounded to ~20 s.
@@ -105,7 +109,7 @@ def stage_bytes(n_touched: int) -> dict:
 
 
 # rocprofv3 kernel names of the stages (substring match on the demangled name)
-STAGE_KERNELS = {"route_norm": "route", "gateup": "gateup_act_kernel", "down": "down_kernel",
+STAGE_KERNELS = {"route_norm": "route", "gateup": "gateup_", "down": "down_kernel",
                  "ffn": "ffn_kernel", "combine": "combine_kernel"}
 
 
