@@ -32,8 +32,10 @@
 //
 // Work split: one workgroup per (expert, column block) walks all rows routed
 // to its expert (sorted slots offsets[e] .. offsets[e+1]) in chunks of up to 32
-// rows for gate/up (one or two 16-row M tiles) and 64 rows for down. Above
-// 8192 routed rows both GEMMs run the GEMM-form row-block kernels of
+// rows for gate/up (one or two 16-row M tiles) and 64 rows for down; with more
+// gate/up items than CUs, one persistent gate/up workgroup per CU walks
+// several of them through one LDS ring (gateup_flow_kernel). Above 8192
+// routed rows both GEMMs run the GEMM-form row-block kernels of
 // moe_rbgemm.hip instead. Workgroups are remapped so that all column blocks
 // of an expert run on the same XCD (shared L2 for its activations).
 
@@ -480,13 +482,14 @@ __global__ __launch_bounds__((NC + NP) * kWave) void gateup_act_kernel(GuArgs A)
 // follow those of its partner, so they stay together on one XCD.
 // Arithmetic and outputs are those of gateup_act_kernel, bit for bit.
 constexpr int kFlowMaxItems = 64;  // items per workgroup (table entries)
+constexpr int kFlowR = 3;          // ring depth
+constexpr int kFlowMinG = 8;       // groups per pass: the next pass's token ids go
+                                   // to LDS at group G/2, its first issue is at G-2
+
 // int32 read through the constant address space: uniform loads become scalar
 // loads (counted by lgkmcnt, not by the vmcnt of the direct-to-LDS loads)
 using ConstI32 = const int32_t __attribute__((address_space(4)));
 __device__ __forceinline__ const ConstI32* as_scalar_i32(const int32_t* p) { return (const ConstI32*)p; }
-constexpr int kFlowR = 3;          // ring depth
-constexpr int kFlowMinG = 8;       // groups per pass: the next pass's token ids go
-                                   // to LDS at group G/2, its first issue is at G-2
 
 template <int NC>
 struct GuFlowShape {
