@@ -464,6 +464,34 @@ def test_layer_256_canvas(gpu):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+def test_layer_256_graph_replays_match_eager(gpu):
+    """The 256-token layer (its persistent gate/up launch included) captured in
+    a HIP graph: every replay, with eager layers on other inputs run in
+    between, gives the eager call's bits."""
+    layer = load_mod("layer")
+    wl = load_mod("workloads")
+    x, nw, ids, w = wl.layer_inputs(256, 7)
+    x2, _, ids2, w2 = wl.layer_inputs(256, 8)
+    expg = wl.make_experts(128, 2816, 704, 7, act="silu").to(gpu)
+    xg, nwg, idsg, wg_ = x.to(gpu), nw.to(gpu), ids.to(gpu), w.to(gpu)
+    y_ref = layer.moe_layer(xg, nwg, 1e-6, expg, idsg, wg_).clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y_g = layer.moe_layer(xg, nwg, 1e-6, expg, idsg, wg_)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for r in range(4):
+        y_other = layer.moe_layer(x2.to(gpu), nwg, 1e-6, expg, ids2.to(gpu), w2.to(gpu))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_g.view(torch.int16), y_ref.view(torch.int16)), f"replay {r}"
+        assert not torch.equal(y_other.view(torch.int16), y_ref.view(torch.int16))
+
+
 def test_prefill_8192_zipf_sampled_tokens(gpu):
     """T = 8192 with Zipf(1.1) expert popularity: large per-expert row counts.
     Rows are independent, so the oracle is evaluated on a sample of tokens."""
