@@ -45,6 +45,7 @@ __device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to
 extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
 extern "C" __device__ __attribute__((const)) float __ockl_wfred_add_f32(float);
 extern "C" __device__ __attribute__((const)) unsigned long long __ockl_wfred_max_u64(unsigned long long);
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_max_i32(int);
 
 __device__ __forceinline__ uint16_t f16_bits(f16 h) { return __builtin_bit_cast(uint16_t, h); }
 

@@ -15,22 +15,27 @@
 // v_mfma_f32_16x16x32_bf16, the K steps split over the waves; the scores go to
 // the probabilities buffer. Then one wave per token does softmax (in place),
 // top-k and the renormalisation in registers.
+#include <cmath>
+#include <utility>
+
 #include "ksl_common.h"
 
 namespace ksl {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kRtWaves = 16;           // one token row per wave in the scores launch
+constexpr int kRtWaves = 16;
 constexpr int kRtThreads = kRtWaves * kWave;
-constexpr int kRtRows = 16;           // tokens per workgroup (one MFMA M tile)
+constexpr int kRtRows = 8;                         // tokens per workgroup: one per normalising wave
+constexpr int kRtLoad = kRtWaves - kRtRows;        // waves 0..7 load the projection and multiply
 constexpr int kRtMaxH = 4096;
 constexpr int kRtMaxE = 256;
 constexpr int kRtMaxK = 16;
-constexpr int kRtRowPad = 16;         // bytes of padding per LDS row
-constexpr int kRtKPer = (kRtMaxH / 32 + kRtWaves - 1) / kRtWaves;  // K steps per wave at most
-constexpr int kRtKEarly = 4;                                        // of them loaded before the row
+constexpr int kRtRowPad = 16;                      // bytes of padding per LDS row
+constexpr int kRtKPer = kRtMaxH / 32 / kRtLoad;    // K steps per loading wave at most
 
 struct RouterArgs {
     const char* x;         // [T, H] bf16 / fp16, row stride xs elements
@@ -42,125 +47,155 @@ struct RouterArgs {
     int64_t* topk_ids;     // [T, k]
     int64_t xs;
     float eps;
+    float root;            // fp32(H ** -0.5)
     int T, H, E, k;
 };
 
-// bf16 rounding (round to nearest even) by the gfx950 conversion instruction:
-// the same value as bf16r for every non-NaN input (fp32 denormals are kept,
-// .amdhsa_float_denorm_mode_32 = 3); a NaN stays a NaN. Used for the router's
-// intermediate activations, where only finite values are observable.
-__device__ __forceinline__ float bf16r_hw(float v) {
-    return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v))) << 16);
+// Two floats to two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32,
+// packed, a in the low half: the same values as bf16r for every non-NaN input
+// (fp32 denormals are kept, .amdhsa_float_denorm_mode_32 = 3); a NaN stays a
+// NaN. Used for the router's intermediate activations, where only finite
+// values are observable.
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// Scores of 16 tokens x 16 experts per workgroup (grid: token blocks x expert
-// tiles), 16 waves: each wave first issues its share of the projection tile
-// (K steps w, w+16, ...: at most kRtKPer per wave, all in flight at once), then
-// normalises one token row into LDS; after a barrier it multiplies its K steps
-// with v_mfma_f32_16x16x32_bf16, and wave 0 sums the 16 partial tiles in a
-// fixed order and stores the bf16-rounded scores as fp32 into probs.
-template <int XD>
+// Scores of 8 tokens x 16 experts per workgroup (grid: token blocks x expert
+// tiles), 16 waves in two roles, so that the waves that stream the projection
+// (2*16*H bytes per workgroup, the bulk of its reads) never hold up the
+// normalisation:
+//  - waves 8..15 normalise token rows 0..7, one each, in the RMSNorm kernels'
+//    layout and order (8 columns per lane and step, an fma chain over the
+//    steps, a fixed xor tree over the lanes: r has the bits of the fused
+//    RMSNorm's), apply the router scale and H^-1/2 and write the bf16 rows to
+//    LDS (padded: the MFMA operand reads are conflict-free);
+//  - waves 0..7 load the projection fragments of K steps g, g + 8, ... for
+//    g = wave (KPER = ceil(H/256) of them, a template parameter so that the
+//    registers held are those the row needs, all in flight at once; no load
+//    predicated, so the compiler waits for each by count), and once the rows
+//    are in LDS multiply them with v_mfma_f32_16x16x32_bf16 (tokens in MFMA
+//    rows 0..7).
+// The row loads are issued before a first barrier and the projection loads
+// after it: a CU serves its loads in issue order. 128 threads then add the 8
+// partial tiles of their (token, expert) in order and store the bf16-rounded
+// score as fp32 into probs.
+template <int XD, int KPER>
 __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
+    constexpr int NS = (KPER + 1) / 2;  // 512-column steps covering the row
     const int H = A.H, E = A.E;
     const int row_bytes = H * 2 + kRtRowPad;
-    char* hrows = lds;                                                   // [16][row_bytes] bf16
-    f32x4* part = reinterpret_cast<f32x4*>(lds + kRtRows * row_bytes);  // [kRtWaves][64]
-    uint16_t* scl = reinterpret_cast<uint16_t*>(part + kRtWaves * kWave);  // [H] router scale
-    const int wave = threadIdx.x / kWave;
+    char* hrows = lds;                                                  // [8][row_bytes] bf16
+    f32x4* part = reinterpret_cast<f32x4*>(lds + kRtRows * row_bytes);  // [kRtLoad][32]
+    const int wave = wave_id();
     const int lane = threadIdx.x & (kWave - 1);
     const int t0 = blockIdx.x * kRtRows;
-    const int tile = blockIdx.y;
-    const float root_py = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(H)));  // fp32(H ** -0.5)
-    const int col = lane & 15, c = lane >> 4;
+    const int e0 = blockIdx.y * 16;
     const int ksteps = H / 32;
+    const int rr = wave - kRtLoad;  // row of a normalising wave
 
-    // 1. the projection fragments of this wave's K steps (independent of the
-    //    rows): the first kRtKEarly now (all of them up to H = 2048), the rest
-    //    once the row's registers are free
-    const uint16_t* prow = A.proj + static_cast<int64_t>(tile * 16 + col) * H + c * 8;
-    u32x4 b[kRtKPer];
-    auto load_b = [&](int u) {
-        int i = wave + u * kRtWaves;
-        if (i >= ksteps) i = wave;  // clamped, never used
-        b[u] = *reinterpret_cast<const u32x4*>(prow + i * 32);
-    };
-#pragma unroll
-    for (int u = 0; u < kRtKEarly; ++u) load_b(u);
-
-    // 2. token row t0 + wave: lane owns columns s*512 + lane*8 .. +8; the
-    //    router scale goes to LDS once per workgroup
-    {
-        const int rr = wave;
+    Raw8<XD> xv[NS];
+    u32x4 sv[NS];
+    if (wave >= kRtLoad) {
         const int t = t0 + rr < A.T ? t0 + rr : A.T - 1;  // rows past T: computed, never stored
         const char* xr = A.x + static_cast<int64_t>(t) * A.xs * 2;
-        Raw8<XD> xv[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < NS; ++s) {  // not predicated: past the row end column 0, dropped
             const int c0 = s * 8 * kWave + lane * 8;
-            xv[s] = c0 < H ? raw_load8<XD>(xr + c0 * 2) : Raw8<XD>{};
+            const int cc = c0 < H ? c0 : 0;
+            xv[s] = raw_load8<XD>(xr + cc * 2);
+            sv[s] = *reinterpret_cast<const u32x4*>(A.scale + cc);
         }
-        if (static_cast<int>(threadIdx.x) * 8 < H)
-            *reinterpret_cast<u32x4*>(scl + threadIdx.x * 8) = *reinterpret_cast<const u32x4*>(A.scale + threadIdx.x * 8);
-        __syncthreads();
+    }
+    dma_barrier();
+
+    const int col = lane & 15, c = lane >> 4;
+    u32x4 b[KPER];
+    if (wave < kRtLoad) {
+        const uint16_t* prow = A.proj + static_cast<int64_t>(e0 + col) * H + c * 8;
+#pragma unroll
+        for (int u = 0; u < KPER; ++u) {  // a step past the end reloads the last one, unused
+            const int i = wave + u * kRtLoad;
+            b[u] = *reinterpret_cast<const u32x4*>(prow + (i < ksteps ? i : ksteps - 1) * 32);
+        }
+    } else {
         float ss = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) ss = rms_sumsq8<XD>(xv[s], ss);
+        for (int s = 0; s < NS; ++s) {
+            if (s * 8 * kWave + lane * 8 >= H) xv[s] = Raw8<XD>{};  // past the row end: exact zeros
+            ss = rms_sumsq8<XD>(xv[s], ss);
+        }
         const float r = rms_scale(ss, 6, H, A.eps);
+        const float root_py = A.root;
+        char* hr = hrows + rr * row_bytes;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < NS; ++s) {
             const int c0 = s * 8 * kWave + lane * 8;
             if (c0 >= H) continue;
             float xf[8], sc[8];
             raw_unpack8<XD>(xv[s], xf);
-            raw_unpack8<KSL_DTYPE_BF16>(Raw8<KSL_DTYPE_BF16>{{*reinterpret_cast<const u32x4*>(scl + c0)}}, sc);
+            raw_unpack8<KSL_DTYPE_BF16>(Raw8<KSL_DTYPE_BF16>{{sv[s]}}, sc);
             u32x4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float h0 = bf16r_hw(bf16r_hw(bf16r_hw(xf[2 * j] * r) * sc[2 * j]) * root_py);
-                const float h1 = bf16r_hw(bf16r_hw(bf16r_hw(xf[2 * j + 1] * r) * sc[2 * j + 1]) * root_py);
-                o[j] = (__float_as_uint(h0) >> 16) | (__float_as_uint(h1) & 0xFFFF0000u);
+                const uint32_t y = bf16x2_rne(xf[2 * j] * r, xf[2 * j + 1] * r);
+                const uint32_t z = bf16x2_rne(__uint_as_float(y << 16) * sc[2 * j],
+                                              __uint_as_float(y & 0xFFFF0000u) * sc[2 * j + 1]);
+                o[j] = bf16x2_rne(__uint_as_float(z << 16) * root_py, __uint_as_float(z & 0xFFFF0000u) * root_py);
             }
-            *reinterpret_cast<u32x4*>(hrows + rr * row_bytes + c0 * 2) = o;
+            *reinterpret_cast<u32x4*>(hr + c0 * 2) = o;
         }
     }
-    if (ksteps > kRtKEarly * kRtWaves) {
-#pragma unroll
-        for (int u = kRtKEarly; u < kRtKPer; ++u) load_b(u);
-    }
-    __syncthreads();
+    lds_sync();
 
-    // 3. this wave's K steps, then the fixed-order sum of the 16 partial tiles
-    const char* arow = hrows + col * row_bytes + c * 16;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (wave < kRtLoad) {
+        // A fragment: lane holds token row col % 8, K columns c*8 .. +8 (MFMA rows
+        // 8..15 repeat rows 0..7; their outputs are not used). Steps u <
+        // KPER - 1 exist for every wave, the last one for waves < ksteps % 8.
+        const char* arow = hrows + (col & (kRtRows - 1)) * row_bytes + c * 16;
+        u32x4 a[KPER];
 #pragma unroll
-    for (int u = 0; u < kRtKPer; ++u) {
-        const int i = wave + u * kRtWaves;
-        if (i < ksteps) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(arow + i * 64);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                           __builtin_bit_cast(bf16x8, b[u]), acc, 0, 0, 0);
+        for (int u = 0; u < KPER; ++u) {
+            const int i = wave + u * kRtLoad;
+            a[u] = *reinterpret_cast<const u32x4*>(arow + (i < ksteps ? i : 0) * 64);
         }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < KPER - 1; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[u]),
+                                                           __builtin_bit_cast(bf16x8, b[u]), acc, 0, 0, 0);
+        if (wave + (KPER - 1) * kRtLoad < ksteps)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[KPER - 1]),
+                                                           __builtin_bit_cast(bf16x8, b[KPER - 1]), acc, 0, 0, 0);
+        // D: lane l < 32 holds tokens 4*(l/16) .. +3 of expert column l % 16
+        if (lane < 32) part[wave * 32 + lane] = acc;
     }
-    part[wave * kWave + lane] = acc;
-    __syncthreads();
-    // thread u < 256 sums element (lane u/4, register u%4) over the waves in order;
-    // D: lane l holds expert tile*16 + l%16, rows 4*(l/16) .. +3; scores rounded to bf16
-    if (threadIdx.x < 4 * kWave) {
-        const int l = threadIdx.x >> 2, q = threadIdx.x & 3;
-        const float* pf = reinterpret_cast<const float*>(part);
-        float sum = pf[l * 4 + q];
-        for (int w = 1; w < kRtWaves; ++w) sum += pf[(w * kWave + l) * 4 + q];
-        const int t = t0 + 4 * (l >> 4) + q;
-        if (t < A.T) A.probs[static_cast<int64_t>(t) * E + tile * 16 + (l & 15)] = bf16r(sum);
+    lds_sync();
+    const int u = static_cast<int>(threadIdx.x) - kRtLoad * kWave;
+    if (u >= 0 && u < kRtRows * 16) {
+        const int tt = u >> 4, e = u & 15;
+        const float* pf = reinterpret_cast<const float*>(part) + ((tt >> 2) * 16 + e) * 4 + (tt & 3);
+        float sum = pf[0];
+#pragma unroll
+        for (int g = 1; g < kRtLoad; ++g) sum += pf[g * 32 * 4];
+        if (t0 + tt < A.T) A.probs[static_cast<int64_t>(t0 + tt) * E + e0 + e] = bf16r(sum);
     }
 }
 
+size_t router_lds_bytes(int H) {
+    return static_cast<size_t>(kRtRows) * (H * 2 + kRtRowPad) + static_cast<size_t>(kRtLoad) * 32 * 16;
+}
+
 // One wave per token: softmax over the scores in probs (in place), then k
-// rounds of a wave arg-max on 64-bit keys (probability bits, then the inverted
-// id: the larger probability wins, equal probabilities go to the lower id),
-// renormalisation and the per-expert scale. Lane l owns entries n = j*64 + l.
+// rounds of selection: the wave max of the probability bits (as int: the
+// probabilities are >= 0, taken entries -1, entries past E -2), then the
+// lowest id holding it (one ballot per lane slot: ids n = j*64 + lane rise
+// with j, then with the lane) — the larger probability first, equal
+// probabilities to the lower id. Renormalisation in rank order, each rank's
+// lane reading its expert's scale from the lane that loaded it.
 constexpr int kTkWaves = 4;
+template <int J>
 __global__ __launch_bounds__(kTkWaves * kWave) void router_topk_kernel(RouterArgs A) {
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
@@ -168,59 +203,94 @@ __global__ __launch_bounds__(kTkWaves * kWave) void router_topk_kernel(RouterArg
     if (t >= A.T) return;
     const int E = A.E;
     float* row = A.probs + static_cast<int64_t>(t) * E;
-    constexpr int J = kRtMaxE / kWave;
-    float s[J];
+    float s[J], pe[J];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
+    for (int j = 0; j < J; ++j) {  // loads not predicated: past E the last entry, dropped
         const int n = j * kWave + lane;
-        s[j] = n < E ? row[n] : -INFINITY;
+        const int nc = n < E ? n : E - 1;
+        s[j] = row[nc];
+        pe[j] = bf16_bits_to_f32(A.pes[nc]);
+        if (n >= E) s[j] = -INFINITY;
         mx = fmaxf(mx, s[j]);
     }
     mx = __ockl_wfred_max_f32(mx);
-    float part = 0.0f;
+    float psum = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int n = j * kWave + lane;
         s[j] = n < E ? expf(s[j] - mx) : 0.0f;
-        part += s[j];
+        psum += s[j];
     }
-    const float sum = __ockl_wfred_add_f32(part);
-    unsigned long long key[J];
+    const float sum = __ockl_wfred_add_f32(psum);
+    int key[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int n = j * kWave + lane;
         s[j] = s[j] / sum;  // probabilities (>= 0)
         if (n < E) row[n] = s[j];
-        key[j] = n < E ? (static_cast<unsigned long long>(__float_as_uint(s[j])) << 32) | (0xFFFFFFFFu - n) : 0ull;
+        key[j] = n < E ? __float_as_int(s[j]) : -2;
     }
+    // rounds without branches: the id is picked with scalar selects, and the
+    // per-expert scale is fetched once at the end by the lane of each rank
     float my_v = 0.0f, wsum = 0.0f;
     int my_i = 0;
     for (int r = 0; r < A.k; ++r) {
-        unsigned long long best = 0ull;
+        int m = key[0];
 #pragma unroll
-        for (int j = 0; j < J; ++j) best = key[j] > best ? key[j] : best;
-        best = __ockl_wfred_max_u64(best);
-        const float v = __uint_as_float(static_cast<uint32_t>(best >> 32));
-        const int n = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best));
+        for (int j = 1; j < J; ++j) m = key[j] > m ? key[j] : m;
+        const int best = __ockl_wfred_max_i32(m);
+        int id = 0;
+#pragma unroll
+        for (int j = J - 1; j >= 0; --j) {  // the lowest slot with a hit wins
+            const unsigned long long hit = __ballot(key[j] == best);
+            const int cand = j * kWave + __ffsll(static_cast<long long>(hit)) - 1;
+            id = hit != 0ull ? cand : id;
+        }
 #pragma unroll
         for (int j = 0; j < J; ++j)
-            if (key[j] == best) key[j] = 0ull;  // taken
+            if (j * kWave + lane == id) key[j] = -1;  // taken
+        const float v = __int_as_float(best);
         if (lane == r) {
             my_v = v;
-            my_i = n;
+            my_i = id;
         }
         wsum += v;
     }
+    float my_sc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const float pj = __shfl(pe[j], my_i & (kWave - 1), kWave);
+        if ((my_i >> 6) == j) my_sc = pj;
+    }
     if (lane < A.k) {
-        A.topk_w[static_cast<int64_t>(t) * A.k + lane] = my_v / wsum * bf16_bits_to_f32(A.pes[my_i]);
+        A.topk_w[static_cast<int64_t>(t) * A.k + lane] = my_v / wsum * my_sc;
         A.topk_ids[static_cast<int64_t>(t) * A.k + lane] = my_i;
     }
 }
 
-size_t router_lds_bytes(int H) {
-    return static_cast<size_t>(kRtRows) * (H * 2 + kRtRowPad) + static_cast<size_t>(kRtWaves) * kWave * 16 +
-           static_cast<size_t>(H) * 2;
+template <int... I>
+void set_scores_attr(bool& ok, std::integer_sequence<int, I...>) {
+    auto one = [&](auto kernel) {
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    };
+    (one(&router_scores_kernel<KSL_DTYPE_BF16, I + 1>), ...);
+    (one(&router_scores_kernel<KSL_DTYPE_F16, I + 1>), ...);
+}
+
+template <int... I>
+void launch_scores(int xd, int kper, dim3 grid, size_t lds, const RouterArgs& A, hipStream_t st,
+                   std::integer_sequence<int, I...>) {
+    auto one = [&](auto kp) {
+        constexpr int KP = decltype(kp)::value;
+        if (kper != KP) return;
+        if (xd == KSL_DTYPE_BF16)
+            hipLaunchKernelGGL((router_scores_kernel<KSL_DTYPE_BF16, KP>), grid, dim3(kRtThreads), lds, st, A);
+        else
+            hipLaunchKernelGGL((router_scores_kernel<KSL_DTYPE_F16, KP>), grid, dim3(kRtThreads), lds, st, A);
+    };
+    (one(std::integral_constant<int, I + 1>{}), ...);
 }
 
 }  // namespace
@@ -247,28 +317,27 @@ int launch_router(const void* x, int xd, int64_t xs, const void* scale, const vo
     A.topk_ids = topk_ids;
     A.xs = xs;
     A.eps = eps;
+    A.root = static_cast<float>(1.0 / std::sqrt(static_cast<double>(H)));  // correctly rounded, as in the module
     A.T = static_cast<int>(T);
     A.H = static_cast<int>(H);
     A.E = static_cast<int>(E);
     A.k = static_cast<int>(k);
-    const size_t lds = router_lds_bytes(A.H);
     const dim3 grid1(static_cast<unsigned>((T + kRtRows - 1) / kRtRows), static_cast<unsigned>(E / 16));
     static const bool attr = [] {
-        const bool a = hipFuncSetAttribute(reinterpret_cast<const void*>(&router_scores_kernel<KSL_DTYPE_BF16>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-        const bool b = hipFuncSetAttribute(reinterpret_cast<const void*>(&router_scores_kernel<KSL_DTYPE_F16>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        bool ok = true;
+        set_scores_attr(ok, std::make_integer_sequence<int, kRtKPer>{});
         (void)hipGetLastError();
-        return a && b;
+        return ok;
     }();
     (void)attr;
-    if (xd == KSL_DTYPE_BF16)
-        hipLaunchKernelGGL((router_scores_kernel<KSL_DTYPE_BF16>), grid1, dim3(kRtThreads), lds, st, A);
-    else
-        hipLaunchKernelGGL((router_scores_kernel<KSL_DTYPE_F16>), grid1, dim3(kRtThreads), lds, st, A);
+    const int kper = (A.H / 32 + kRtLoad - 1) / kRtLoad;  // K steps per loading wave, 1..16
+    launch_scores(xd, kper, grid1, router_lds_bytes(A.H), A, st, std::make_integer_sequence<int, kRtKPer>{});
     KSL_LAUNCH_CHECK();
     const unsigned grid2 = static_cast<unsigned>((T + kTkWaves - 1) / kTkWaves);
-    hipLaunchKernelGGL(router_topk_kernel, dim3(grid2), dim3(kTkWaves * kWave), 0, st, A);
+    if (E <= 2 * kWave)
+        hipLaunchKernelGGL((router_topk_kernel<2>), dim3(grid2), dim3(kTkWaves * kWave), 0, st, A);
+    else
+        hipLaunchKernelGGL((router_topk_kernel<kRtMaxE / kWave>), dim3(grid2), dim3(kTkWaves * kWave), 0, st, A);
     KSL_LAUNCH_CHECK();
     return KSL_OK;
 }
