@@ -65,25 +65,28 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
 // tiles), 16 waves in two roles, so that the waves that stream the projection
 // (2*16*H bytes per workgroup, the bulk of its reads) never hold up the
 // normalisation:
-//  - waves 8..15 normalise token rows 0..7, one each, in the RMSNorm kernels'
+//  - waves 0..7 normalise token rows 0..7, one each, in the RMSNorm kernels'
 //    layout and order (8 columns per lane and step, an fma chain over the
 //    steps, a fixed xor tree over the lanes: r has the bits of the fused
 //    RMSNorm's), apply the router scale and H^-1/2 and write the bf16 rows to
-//    LDS (padded: the MFMA operand reads are conflict-free);
-//  - waves 0..7 load the projection fragments of K steps g, g + 8, ... for
-//    g = wave (KPER = ceil(H/256) of them, a template parameter so that the
-//    registers held are those the row needs, all in flight at once; no load
-//    predicated, so the compiler waits for each by count), and once the rows
-//    are in LDS multiply them with v_mfma_f32_16x16x32_bf16 (tokens in MFMA
-//    rows 0..7).
+//    LDS (padded: the MFMA operand reads are conflict-free), the first half of
+//    the column steps, a barrier, then the rest;
+//  - waves 8..15 load the projection fragments of K steps g, g + 8, ... for
+//    g = wave - 8 (KPER = ceil(H/256) of them, a template parameter so that
+//    the registers held are those the row needs, all in flight at once; no
+//    load predicated, so the compiler waits for each by count), multiply the
+//    first half of the rows with v_mfma_f32_16x16x32_bf16 (tokens in MFMA rows
+//    0..7) while the second half is normalised, then the rest.
 // The row loads are issued before a first barrier and the projection loads
-// after it: a CU serves its loads in issue order. 128 threads then add the 8
-// partial tiles of their (token, expert) in order and store the bf16-rounded
-// score as fp32 into probs.
+// after it, so the rows are not queued behind the projection (a CU serves its
+// loads in issue order); no barrier waits for global loads. 128 threads then add
+// the 8 partial tiles of their (token, expert) in order and store the
+// bf16-rounded score as fp32 into probs.
 template <int XD, int KPER>
 __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     constexpr int NS = (KPER + 1) / 2;  // 512-column steps covering the row
+    constexpr int NS1 = NS / 2;         // of them normalised before the first MFMAs
     const int H = A.H, E = A.E;
     const int row_bytes = H * 2 + kRtRowPad;
     char* hrows = lds;                                                  // [8][row_bytes] bf16
@@ -93,13 +96,14 @@ __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A)
     const int t0 = blockIdx.x * kRtRows;
     const int e0 = blockIdx.y * 16;
     const int ksteps = H / 32;
-    const int rr = wave - kRtLoad;  // row of a normalising wave
+    const int col = lane & 15, c = lane >> 4;
 
-    Raw8<XD> xv[NS];
-    u32x4 sv[NS];
-    if (wave >= kRtLoad) {
-        const int t = t0 + rr < A.T ? t0 + rr : A.T - 1;  // rows past T: computed, never stored
+    if (wave < kRtRows) {
+        // normalising wave: token row t0 + wave, lane owns columns s*512 + lane*8 .. +8
+        const int t = t0 + wave < A.T ? t0 + wave : A.T - 1;  // rows past T: computed, never stored
         const char* xr = A.x + static_cast<int64_t>(t) * A.xs * 2;
+        Raw8<XD> xv[NS];
+        u32x4 sv[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {  // not predicated: past the row end column 0, dropped
             const int c0 = s * 8 * kWave + lane * 8;
@@ -107,19 +111,7 @@ __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A)
             xv[s] = raw_load8<XD>(xr + cc * 2);
             sv[s] = *reinterpret_cast<const u32x4*>(A.scale + cc);
         }
-    }
-    dma_barrier();
-
-    const int col = lane & 15, c = lane >> 4;
-    u32x4 b[KPER];
-    if (wave < kRtLoad) {
-        const uint16_t* prow = A.proj + static_cast<int64_t>(e0 + col) * H + c * 8;
-#pragma unroll
-        for (int u = 0; u < KPER; ++u) {  // a step past the end reloads the last one, unused
-            const int i = wave + u * kRtLoad;
-            b[u] = *reinterpret_cast<const u32x4*>(prow + (i < ksteps ? i : ksteps - 1) * 32);
-        }
-    } else {
+        dma_barrier();  // every row load is queued before the first projection load
         float ss = 0.0f;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -128,11 +120,10 @@ __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A)
         }
         const float r = rms_scale(ss, 6, H, A.eps);
         const float root_py = A.root;
-        char* hr = hrows + rr * row_bytes;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
+        char* hr = hrows + wave * row_bytes;
+        auto norm_step = [&](int s) {
             const int c0 = s * 8 * kWave + lane * 8;
-            if (c0 >= H) continue;
+            if (c0 >= H) return;
             float xf[8], sc[8];
             raw_unpack8<XD>(xv[s], xf);
             raw_unpack8<KSL_DTYPE_BF16>(Raw8<KSL_DTYPE_BF16>{{sv[s]}}, sc);
@@ -145,36 +136,59 @@ __global__ __launch_bounds__(kRtThreads) void router_scores_kernel(RouterArgs A)
                 o[j] = bf16x2_rne(__uint_as_float(z << 16) * root_py, __uint_as_float(z & 0xFFFF0000u) * root_py);
             }
             *reinterpret_cast<u32x4*>(hr + c0 * 2) = o;
-        }
-    }
-    lds_sync();
-
-    if (wave < kRtLoad) {
-        // A fragment: lane holds token row col % 8, K columns c*8 .. +8 (MFMA rows
-        // 8..15 repeat rows 0..7; their outputs are not used). Steps u <
-        // KPER - 1 exist for every wave, the last one for waves < ksteps % 8.
-        const char* arow = hrows + (col & (kRtRows - 1)) * row_bytes + c * 16;
-        u32x4 a[KPER];
+        };
+#pragma unroll
+        for (int s = 0; s < NS1; ++s) norm_step(s);
+        lds_sync();
+#pragma unroll
+        for (int s = NS1; s < NS; ++s) norm_step(s);
+        lds_sync();
+    } else {
+        // loading wave g: K steps g, g + 8, ... (a step past the end reloads the
+        // last one, unused); A fragment: lane holds token row col % 8, K columns
+        // c*8 .. +8 (MFMA rows 8..15 repeat rows 0..7; their outputs are not
+        // used). Steps u < 2*NS1 lie in the rows' first NS1 column steps and are
+        // multiplied while the rest is normalised; steps u < KPER - 1 exist for
+        // every wave, the last one for waves g < ksteps % 8.
+        const int g = wave - kRtRows;
+        const uint16_t* prow = A.proj + static_cast<int64_t>(e0 + col) * H + c * 8;
+        u32x4 b[KPER];
+        dma_barrier();
 #pragma unroll
         for (int u = 0; u < KPER; ++u) {
-            const int i = wave + u * kRtLoad;
-            a[u] = *reinterpret_cast<const u32x4*>(arow + (i < ksteps ? i : 0) * 64);
+            const int i = g + u * kRtLoad;
+            b[u] = *reinterpret_cast<const u32x4*>(prow + (i < ksteps ? i : ksteps - 1) * 32);
         }
+        const char* arow = hrows + (col & (kRtRows - 1)) * row_bytes + c * 16;
+        u32x4 a[KPER];
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        lds_sync();
 #pragma unroll
-        for (int u = 0; u < KPER - 1; ++u)
+        for (int u = 0; u < 2 * NS1; ++u) a[u] = *reinterpret_cast<const u32x4*>(arow + (g + u * kRtLoad) * 64);
+#pragma unroll
+        for (int u = 0; u < 2 * NS1; ++u)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[u]),
                                                            __builtin_bit_cast(bf16x8, b[u]), acc, 0, 0, 0);
-        if (wave + (KPER - 1) * kRtLoad < ksteps)
+        asm volatile("" : "+v"(acc));  // these MFMAs before the barrier, not after it
+        lds_sync();
+#pragma unroll
+        for (int u = 2 * NS1; u < KPER; ++u) {
+            const int i = g + u * kRtLoad;
+            a[u] = *reinterpret_cast<const u32x4*>(arow + (i < ksteps ? i : 0) * 64);
+        }
+#pragma unroll
+        for (int u = 2 * NS1; u < KPER - 1; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[u]),
+                                                           __builtin_bit_cast(bf16x8, b[u]), acc, 0, 0, 0);
+        if (g + (KPER - 1) * kRtLoad < ksteps)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[KPER - 1]),
                                                            __builtin_bit_cast(bf16x8, b[KPER - 1]), acc, 0, 0, 0);
         // D: lane l < 32 holds tokens 4*(l/16) .. +3 of expert column l % 16
-        if (lane < 32) part[wave * 32 + lane] = acc;
+        if (lane < 32) part[g * 32 + lane] = acc;
     }
     lds_sync();
-    const int u = static_cast<int>(threadIdx.x) - kRtLoad * kWave;
-    if (u >= 0 && u < kRtRows * 16) {
-        const int tt = u >> 4, e = u & 15;
+    if (threadIdx.x < kRtRows * 16) {
+        const int tt = threadIdx.x >> 4, e = threadIdx.x & 15;
         const float* pf = reinterpret_cast<const float*>(part) + ((tt >> 2) * 16 + e) * 4 + (tt & 3);
         float sum = pf[0];
 #pragma unroll
