@@ -209,6 +209,39 @@ size_t router_lds_bytes(int H) {
 // probabilities to the lower id. Renormalisation in rank order, each rank's
 // lane reading its expert's scale from the lane that loaded it.
 constexpr int kTkWaves = 4;
+
+// Wave max of an int or a float, left in every lane, by a butterfly of cross-lane moves
+// (DPP quad_perm for partners l ^ 1 and l ^ 2, quad_perm then row_half_mirror
+// for l ^ 4, row_ror:8 for l ^ 8, v_permlane16_swap / v_permlane32_swap for
+// l ^ 16 and l ^ 32, where each lane ends up with its own value and the
+// partner's): no round trip through scalar registers. A max is exact in any
+// order.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i32(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int wave_max_bfly(int v) {
+    v = max(v, dpp_mov_i32<0xB1>(v));
+    v = max(v, dpp_mov_i32<0x4E>(v));
+    v = max(v, dpp_mov_i32<0x141>(dpp_mov_i32<0x1B>(v)));
+    v = max(v, dpp_mov_i32<0x128>(v));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+    v = max(static_cast<int>(p16[0]), static_cast<int>(p16[1]));
+    const auto p32 = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+    return max(static_cast<int>(p32[0]), static_cast<int>(p32[1]));
+}
+
+__device__ __forceinline__ float wave_max_bfly(float v) {
+    v = fmaxf(v, __int_as_float(dpp_mov_i32<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov_i32<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov_i32<0x141>(dpp_mov_i32<0x1B>(__float_as_int(v)))));
+    v = fmaxf(v, __int_as_float(dpp_mov_i32<0x128>(__float_as_int(v))));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+}
+
 template <int J>
 __global__ __launch_bounds__(kTkWaves * kWave) void router_topk_kernel(RouterArgs A) {
     const int wave = threadIdx.x / kWave;
@@ -228,7 +261,7 @@ __global__ __launch_bounds__(kTkWaves * kWave) void router_topk_kernel(RouterArg
         if (n >= E) s[j] = -INFINITY;
         mx = fmaxf(mx, s[j]);
     }
-    mx = __ockl_wfred_max_f32(mx);
+    mx = wave_max_bfly(mx);
     float psum = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -253,7 +286,7 @@ __global__ __launch_bounds__(kTkWaves * kWave) void router_topk_kernel(RouterArg
         int m = key[0];
 #pragma unroll
         for (int j = 1; j < J; ++j) m = key[j] > m ? key[j] : m;
-        const int best = __ockl_wfred_max_i32(m);
+        const int best = wave_max_bfly(m);
         int id = 0;
 #pragma unroll
         for (int j = J - 1; j >= 0; --j) {  // the lowest slot with a hit wins
