@@ -50,6 +50,9 @@ CASES = [
     (37, 512, 32, 4, 43, torch.bfloat16),      # ragged token count (rows past T in the last workgroup)
     (200, 256, 64, 2, 44, torch.float16),
     (20, 4096, 256, 16, 45, torch.bfloat16),   # largest supported sizes
+    (64, 1056, 128, 8, 48, torch.bfloat16),    # 33 K steps: only the first projection wave has a 5th
+    (16, 2848, 64, 6, 49, torch.bfloat16),     # 89 K steps, 6 column steps with a partial last one
+    (9, 32, 16, 2, 50, torch.float16),         # smallest row (one K step) and one expert tile
 ]
 
 
