@@ -272,13 +272,39 @@ __device__ __forceinline__ float rms_sumsq8(const Raw8<XD>& v, float ss) {
     for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(xf[j], xf[j], ss);
     return ss;
 }
+// Sum over aligned groups of 2^lpr_log2 lanes (lpr_log2 <= 6) by the xor
+// tree v += v[l ^ off], off = 2^(lpr_log2-1) .. 1 in that order: the bits of
+// adding __shfl_xor(v, off) step by step (each step adds the same two values,
+// and the addition commutes), with the partners fetched by cross-lane moves
+// instead of LDS permutes: v_permlane32_swap / v_permlane16_swap for 32 and
+// 16 (every lane then holds its half and the partner's, so their sum is the
+// step's), DPP row_ror:8 for 8, quad_perm then row_half_mirror for 4
+// (l ^ 3 ^ 7), quad_perm for 2 and 1. All lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float xor_tree_sum(float v, int lpr_log2) {
+    if (lpr_log2 >= 6) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    if (lpr_log2 >= 5) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    if (lpr_log2 >= 4) v += dpp_mov<0x128>(v);                 // row_ror:8
+    if (lpr_log2 >= 3) v += dpp_mov<0x141>(dpp_mov<0x1B>(v));  // quad_perm [3,2,1,0], row_half_mirror
+    if (lpr_log2 >= 2) v += dpp_mov<0x4E>(v);                  // quad_perm [2,3,0,1]
+    if (lpr_log2 >= 1) v += dpp_mov<0xB1>(v);                  // quad_perm [1,0,3,2]
+    return v;
+}
 __device__ __forceinline__ float rms_inv(float ss, int cols, float eps) {
     const float ms = ss / static_cast<float>(cols) + eps;
     return 1.0f / __builtin_sqrtf(ms);
 }
 __device__ __forceinline__ float rms_scale(float ss, int lpr_log2, int cols, float eps) {
-    for (int off = (1 << lpr_log2) >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-    return rms_inv(ss, cols, eps);
+    return rms_inv(xor_tree_sum(ss, lpr_log2), cols, eps);
 }
 template <bool HAS_W>
 __device__ __forceinline__ float rms_apply(float x, float r, float w) {
@@ -300,16 +326,21 @@ __device__ __forceinline__ void rms_row(const typename Elem<XD>::T* __restrict__
     const int stride_cols = 8 << lpr_log2;
     Raw8<XD> xv[NSTEP];
     Raw8<WD> wv[HAS_W ? NSTEP : 1];
+    // loads not predicated (a step past the row end, or a row past the last,
+    // reloads column 0 and drops it): predicated loads sit in branches, and the
+    // compiler then waits for every load and store in flight (vmcnt(0)) before
+    // each use instead of counting
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
         const int c0 = s * stride_cols + sl * 8;
-        if (row_ok && c0 < cols) {
-            xv[s] = raw_load8<XD>(xr + c0);
-            if constexpr (HAS_W) wv[s] = raw_load8<WD>(w + c0);
-        } else {
-            xv[s] = Raw8<XD>{};  // zeros
-        }
+        const int cc = row_ok && c0 < cols ? c0 : 0;
+        xv[s] = raw_load8<XD>(xr + cc);
+        if constexpr (HAS_W) wv[s] = raw_load8<WD>(w + cc);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all issued here, not sunk below the sum of squares
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s)
+        if (!(row_ok && s * stride_cols + sl * 8 < cols)) xv[s] = Raw8<XD>{};  // zeros
     float ss = 0.0f;
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) ss = rms_sumsq8<XD>(xv[s], ss);

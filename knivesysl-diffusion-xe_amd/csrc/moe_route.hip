@@ -119,8 +119,9 @@ constexpr int kFastPer = kFastPad / (kFastWaves * kWave); // ids loaded per thre
 // 16-byte groups of 8 keys), so row order is (lane, then position). The
 // expert's first slot is the number of rows with a smaller key (a wave sum of
 // per-lane counts); a lane's first slot adds the expert's rows held by the
-// lanes below it (a wave scan); each lane then places its own rows in order:
-// the stable order of the reference. Wave E writes inv = 0 for dropped rows,
+// lanes below it (an exclusive scan by ballots, one per bit of the count);
+// each lane then places its own rows in order, walking a mask of them: the
+// stable order of the reference. Wave E writes inv = 0 for dropped rows,
 // offsets[E] and the unused tail slots (Nexp).
 __device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, int Nexp, int E,
                                               int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv,
@@ -152,45 +153,46 @@ __device__ __forceinline__ void route_fast_wg(const int64_t* __restrict__ ids, i
     }
     __syncthreads();
     if (e > E) return;
-    // 2. this lane's rows: counts below and at e
+    // 2. this lane's rows: the count below e and a mask of the rows at e
+    //    (at most 64 per lane: Nexp <= kFastRows)
     const int r0 = lane * rpl;
     const u32x4* kq = reinterpret_cast<const u32x4*>(keys + r0);
     const int nq = rpl / 8;
-    int c_lt = 0, c_eq = 0;
+    int c_lt = 0;
+    uint64_t at_e = 0;
     for (int q = 0; q < nq; ++q) {
         const u32x4 v = kq[q];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int k = static_cast<int>((v[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
             c_lt += k < e ? 1 : 0;
-            c_eq += k == e ? 1 : 0;
+            at_e |= static_cast<uint64_t>(k == e ? 1u : 0u) << (q * 8 + j);
         }
     }
+    const int c_eq = __popcll(at_e);
     const int before = __ockl_wfred_add_i32(c_lt);
-    int incl = c_eq;
+    // exclusive prefix of c_eq over the lanes, bit by bit (c_eq <= 64): per
+    // bit, a ballot and the count of its lanes below this one
+    int excl = 0;
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int o = __shfl_up(incl, off, kWave);
-        if (lane >= off) incl += o;
+    for (int b = 0; b < 7; ++b) {
+        const uint64_t bm = __ballot((c_eq >> b) & 1);
+        excl += static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0u)))
+                << b;
     }
-    // 3. scatter in row order
-    int slot = before + incl - c_eq;
-    for (int q = 0; q < nq; ++q) {
-        const u32x4 v = kq[q];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int k = static_cast<int>((v[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-            if (k == e) {
-                const int r = r0 + q * 8 + j;
-                if (e < E) {
-                    sorted_rows[slot] = r;
-                    inv[r] = slot;
-                    ++slot;
-                } else {
-                    inv[r] = 0;
-                }
-            }
+    // 3. scatter in row order: each lane walks only its rows at e
+    int slot = before + excl;
+    while (at_e != 0ull) {
+        const int r = r0 + __ffsll(static_cast<long long>(at_e)) - 1;
+        if (e < E) {
+            sorted_rows[slot] = r;
+            inv[r] = slot;
+            ++slot;
+        } else {
+            inv[r] = 0;
         }
+        at_e &= at_e - 1ull;
     }
     if (lane == 0) offsets[e] = before;
     if (e == E) {

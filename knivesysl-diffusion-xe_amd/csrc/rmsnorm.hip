@@ -61,7 +61,7 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_vec_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(t[j], t[j], ss);
     }
-    for (int off = lpr >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    ss = xor_tree_sum(ss, lpr_log2);
     const float ms = ss / static_cast<float>(cols) + eps;
     const float r = 1.0f / __builtin_sqrtf(ms);
     if (!row_ok) return;
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_scalar_kernel(
         const float t = Elem<XD>::load(xr + c);
         ss = __builtin_fmaf(t, t, ss);
     }
-    for (int off = kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    ss = xor_tree_sum(ss, 6);
     const float r = 1.0f / __builtin_sqrtf(ss / static_cast<float>(cols) + eps);
     YT* yr = y + row * ys;
     for (int c = lane; c < cols; c += kWave) {
