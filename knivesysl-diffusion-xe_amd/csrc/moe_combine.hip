@@ -51,7 +51,10 @@ constexpr int kCombThreads = 256;
 // F16P (the v1 combine, kernels/fused_moe_w4.py:125-127): the weight is
 // rounded to fp16 first and each product w * x to fp16 (torch's fp16 multiply),
 // the products are summed in fp32 in slot order.
-template <int WD, bool F16P = false>
+// WIDE (topk % 8 == 0, inv and w 16-byte aligned: the layer's case): the 8
+// indices and 8 weights of a block in 16-byte loads (4 or 3 instructions
+// instead of 16; every lane of a token loads the same ones), same values.
+template <int WD, bool F16P = false, bool WIDE = false>
 __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const int32_t* __restrict__ inv,
                                             const typename Elem<WD>::T* __restrict__ w, int64_t t, int topk,
                                             int64_t H, int64_t c0, float (&acc)[8]) {
@@ -60,19 +63,45 @@ __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const 
     for (int k0 = 0; k0 < topk; k0 += 8) {
         int32_t r[8];
         float wk[8];
+        if constexpr (WIDE) {
+            const u32x4* ip = reinterpret_cast<const u32x4*>(inv + t * topk + k0);
+            const u32x4 i0 = ip[0], i1 = ip[1];
+            float wr[8];
+            if constexpr (WD == KSL_DTYPE_F32) {
+                const f32x4* wp = reinterpret_cast<const f32x4*>(w + t * topk + k0);
+                const f32x4 w0 = wp[0], w1 = wp[1];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int kk = k0 + k < topk ? k0 + k : topk - 1;
-            r[k] = inv[t * topk + kk];
-            wk[k] = Elem<WD>::load(w + t * topk + kk);
-            if (F16P) wk[k] = static_cast<float>(static_cast<f16>(wk[k]));
+                for (int k = 0; k < 4; ++k) {
+                    wr[k] = w0[k];
+                    wr[4 + k] = w1[k];
+                }
+            } else {
+                raw_unpack8<WD>(raw_load8<WD>(w + t * topk + k0), wr);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                r[k] = static_cast<int32_t>(i0[k]);
+                r[4 + k] = static_cast<int32_t>(i1[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) wk[k] = F16P ? static_cast<float>(static_cast<f16>(wr[k])) : wr[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int kk = k0 + k < topk ? k0 + k : topk - 1;
+                r[k] = inv[t * topk + kk];
+                wk[k] = Elem<WD>::load(w + t * topk + kk);
+                if (F16P) wk[k] = static_cast<float>(static_cast<f16>(wk[k]));
+            }
         }
         f16x8 x[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) x[k] = *reinterpret_cast<const f16x8*>(out3 + static_cast<int64_t>(r[k]) * H + c0);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            if (k0 + k < topk) {
+            // WIDE: every slot of the block is real, so no branch (a branch per
+            // slot let the compiler reload a row inside it, one round trip late)
+            if (WIDE || k0 + k < topk) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     if (F16P)
@@ -85,7 +114,7 @@ __device__ __forceinline__ void combine_acc(const f16* __restrict__ out3, const 
     }
 }
 
-template <int WD, int YD, bool F16P>
+template <int WD, int YD, bool F16P, bool WIDE>
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __restrict__ out3,
                                                               const int32_t* __restrict__ inv,
                                                               const void* __restrict__ wv, int64_t T,
@@ -99,7 +128,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(const f16* __rest
     if (t >= T) return;
     const int64_t c0 = (idx - t * hv) * 8;
     float acc[8];
-    combine_acc<WD, F16P>(out3, inv, static_cast<const typename Elem<WD>::T*>(wv), t, topk, H, c0, acc);
+    combine_acc<WD, F16P, WIDE>(out3, inv, static_cast<const typename Elem<WD>::T*>(wv), t, topk, H, c0, acc);
     if (F16P) {  // the fp16 sum, then .to(y dtype)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = static_cast<float>(static_cast<f16>(acc[j]));
@@ -117,19 +146,24 @@ int launch_combine_y(int yd, const void* out3, const int32_t* inv, const void* w
     const int64_t n = T * (H / 8);
     const unsigned grid = static_cast<unsigned>((n + kCombThreads - 1) / kCombThreads);
     const f16* o3 = static_cast<const f16*>(out3);
+    const bool wide = topk % 8 == 0 && reinterpret_cast<uintptr_t>(inv) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    auto go = [&](auto yd_c, auto wide_c) {
+        constexpr int YDC = decltype(yd_c)::value;
+        constexpr bool WC = decltype(wide_c)::value;
+        hipLaunchKernelGGL((combine_kernel<WD, YDC, F16P, WC>), dim3(grid), dim3(kCombThreads), 0, st, o3, inv, w,
+                           T, static_cast<int>(topk), H, y, ys, err);
+    };
+    auto go_y = [&](auto yd_c) {
+        if (wide)
+            go(yd_c, std::true_type{});
+        else
+            go(yd_c, std::false_type{});
+    };
     switch (yd) {
-        case KSL_DTYPE_BF16:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_BF16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
-            break;
-        case KSL_DTYPE_F16:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F16, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
-            break;
-        case KSL_DTYPE_F32:
-            hipLaunchKernelGGL((combine_kernel<WD, KSL_DTYPE_F32, F16P>), dim3(grid), dim3(kCombThreads), 0, st, o3,
-                               inv, w, T, static_cast<int>(topk), H, y, ys, err);
-            break;
+        case KSL_DTYPE_BF16: go_y(std::integral_constant<int, KSL_DTYPE_BF16>{}); break;
+        case KSL_DTYPE_F16: go_y(std::integral_constant<int, KSL_DTYPE_F16>{}); break;
+        case KSL_DTYPE_F32: go_y(std::integral_constant<int, KSL_DTYPE_F32>{}); break;
         default:
             return KSL_ERR_ARG;
     }
@@ -271,7 +305,7 @@ __device__ __forceinline__ float block_row_sum(float v, float* part, int nwaves)
     return s;
 }
 
-template <int WD>
+template <int WD, bool WIDE>
 __global__ __launch_bounds__(kPostMaxWaves * kWave) void combine_post_kernel(PostArgs A) {
     constexpr int BF = KSL_DTYPE_BF16;
     __shared__ float part[2][kPostMaxWaves];
@@ -293,7 +327,8 @@ __global__ __launch_bounds__(kPostMaxWaves * kWave) void combine_post_kernel(Pos
                                       : bf16_bits_to_f32(*static_cast<const uint16_t*>(A.ls));
     float m[8];
     if (ok) {
-        combine_acc<WD>(A.out3, A.inv, static_cast<const typename Elem<WD>::T*>(A.w), t, A.topk, A.H, c0, m);
+        combine_acc<WD, false, WIDE>(A.out3, A.inv, static_cast<const typename Elem<WD>::T*>(A.w), t, A.topk, A.H,
+                                     c0, m);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) m[j] = 0.0f;
@@ -400,10 +435,19 @@ int launch_combine_post(const void* out3, const int32_t* inv, const void* w, int
     A.ls_dt = ls_dt;
     const int threads = static_cast<int>((H / 8 + kWave - 1) / kWave) * kWave;
     const dim3 grid(static_cast<unsigned>(T)), block(threads);
+    const bool wide = topk % 8 == 0 && reinterpret_cast<uintptr_t>(inv) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    auto go = [&](auto wd_c) {
+        constexpr int WDC = decltype(wd_c)::value;
+        if (wide)
+            hipLaunchKernelGGL((combine_post_kernel<WDC, true>), grid, block, 0, st, A);
+        else
+            hipLaunchKernelGGL((combine_post_kernel<WDC, false>), grid, block, 0, st, A);
+    };
     switch (wd) {
-        case KSL_DTYPE_F32: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_F32>, grid, block, 0, st, A); break;
-        case KSL_DTYPE_F16: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_F16>, grid, block, 0, st, A); break;
-        default: hipLaunchKernelGGL(combine_post_kernel<KSL_DTYPE_BF16>, grid, block, 0, st, A); break;
+        case KSL_DTYPE_F32: go(std::integral_constant<int, KSL_DTYPE_F32>{}); break;
+        case KSL_DTYPE_F16: go(std::integral_constant<int, KSL_DTYPE_F16>{}); break;
+        default: go(std::integral_constant<int, KSL_DTYPE_BF16>{}); break;
     }
     KSL_LAUNCH_CHECK();
     return KSL_OK;
