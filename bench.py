@@ -21,11 +21,18 @@ Timed passes (all inside this process, on one stream):
   1. value: K steps of the layer (one C call per step: routing + RMSNorm +
      fp16 activations, gate/up, down, combine; with --ffn gate/up and down
      are one launch), bracketed by synchronize; µs per layer = elapsed / K.
-  2. per-kernel: each stage's kernel alone, K launches back to back between
+  2. per-kernel: each stage's kernel alone, launches back to back between
      two HIP events on the same stream (the routing produced once; gate/up
-     and down rotate over the weight sets), giving its average launch
-     duration; achieved GB/s = the kernel's algorithmic bytes / that
-     duration, and the dominant kernel's is the roofline. (Inside the layer,
+     and down rotate over the weight sets), timed two ways: K launches from
+     Python one by one (`eager_us`), and 20 launches captured in a HIP graph
+     and replayed K/20 times, at least twice (`graph_us`). `avg_us` is the
+     eager figure for gate/up and down, as the layer launches them, and the
+     replay's for route_norm and combine, whose few microseconds of GPU work
+     are paced by the host's launch cost when launched one by one from
+     Python (a replay of back-to-back down launches reads ~3 us longer than
+     the eager ones, so the expert GEMMs keep the eager figure). Achieved
+     GB/s = the kernel's algorithmic bytes / that duration, and the dominant
+     kernel's is the roofline. (Inside the layer,
      after route_norm, rocprofv3 reads the persistent gate/up kernel's
      dispatches ~4 us shorter than back to back; timing each stage inside the
      layer with events between the launches adds ~2-3 us of launch gap per
@@ -109,6 +116,7 @@ def stage_bytes(n_touched: int) -> dict:
 
 
 # rocprofv3 kernel names of the stages (substring match on the demangled name)
+LATENCY_STAGES = ("route_norm", "combine")  # timed by graph replay (see pass 2)
 STAGE_KERNELS = {"route_norm": "route", "gateup": "gateup_", "down": "down_kernel",
                  "ffn": "ffn_kernel", "combine": "combine_kernel"}
 
@@ -303,6 +311,7 @@ def main() -> int:
             if rc:
                 lib.check(rc, name)
 
+        n_cap = 20
         for name in stages:
             for i in range(args.warmup):
                 launch(name, sets[i % len(sets)])
@@ -313,13 +322,42 @@ def main() -> int:
                 launch(name, sets[i % len(sets)])
             b.record()
             torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / args.steps
+            eager_us = a.elapsed_time(b) * 1e3 / args.steps
+            # the same launches replayed from a graph: no host launch cost between
+            # them (a few-microsecond kernel launched one by one from Python is
+            # paced by the host); no memset nodes, every launch writes its outputs
+            cap_stream = torch.cuda.Stream()
+            cap_stream.wait_stream(torch.cuda.current_stream())
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=cap_stream):
+                st = lib.stream_of(xg)  # the capturing stream
+                for i in range(n_cap):
+                    launch(name, sets[i % len(sets)])
+            st = lib.stream_of(xg)
+            torch.cuda.current_stream().wait_stream(cap_stream)
+            graph.replay()
+            torch.cuda.synchronize()
+            reps = max(2, args.steps // n_cap)
+            a.record()
+            for _ in range(reps):
+                graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            graph_us = a.elapsed_time(b) * 1e3 / (reps * n_cap)
+            del graph
+            # the latency stages (a few microseconds each) are paced by the host's
+            # launch cost when launched one by one: their figure is the replay's;
+            # the expert GEMMs (tens of microseconds) keep the eager launches,
+            # the way the layer launches them
+            us = graph_us if name in LATENCY_STAGES else eager_us
             gbps = sbytes[name] / (us * 1e-6) / 1e9
-            kernels[name] = {"avg_us": round(us, 3), "algorithmic_bytes": sbytes[name], "GBps": round(gbps, 1),
+            kernels[name] = {"avg_us": round(us, 3), "eager_us": round(eager_us, 3), "graph_us": round(graph_us, 3),
+                             "algorithmic_bytes": sbytes[name], "GBps": round(gbps, 1),
                              "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
         tot = sum(v["avg_us"] for v in kernels.values())
-        log("[bench] per-kernel avg us (alone, back to back): "
-            + ", ".join(f"{k} {v['avg_us']:.2f} ({v['GBps']:.0f} GB/s)" for k, v in kernels.items())
+        log("[bench] per-kernel avg us (alone, back to back; eager launches / graph replay in brackets): "
+            + ", ".join(f"{k} {v['avg_us']:.2f} [{v['eager_us']:.2f} / {v['graph_us']:.2f}] ({v['GBps']:.0f} GB/s)"
+                        for k, v in kernels.items())
             + f" (sum {tot:.2f}, layer {layer_us:.2f})")
         # the staged launches give the fused call's bits
         step(sets[0])
