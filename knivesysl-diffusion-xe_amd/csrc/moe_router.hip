@@ -8,12 +8,13 @@
 //   probs  = softmax(fp32(scores))
 //   w, idx = top-k of probs (descending, equal values: lower index first)
 //   w      = w / sum(w) * per_expert_scale[idx]
-// Two launches. Scores: one workgroup of 4 waves per 16 tokens x 16 experts
+// Two launches. Scores: one workgroup of 16 waves per 8 tokens x 16 experts
 // (so the projection, 2*E*H bytes, is spread over E/16 workgroups per token
-// block instead of streaming through one CU): the rows are normalised into LDS
-// (bf16, padded rows: conflict-free MFMA operand reads) and multiplied with
-// v_mfma_f32_16x16x32_bf16, the K steps split over the waves; the scores go to
-// the probabilities buffer. Then one wave per token does softmax (in place),
+// block, and a CU reads 16 projection rows and 8 token rows): 8 waves
+// normalise the rows into LDS (bf16, padded rows: conflict-free MFMA operand
+// reads), 8 waves stream the projection and multiply with
+// v_mfma_f32_16x16x32_bf16, the K steps split over them; the scores go to the
+// probabilities buffer. Then one wave per token does softmax (in place),
 // top-k and the renormalisation in registers.
 #include <cmath>
 #include <utility>
